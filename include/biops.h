@@ -1,0 +1,195 @@
+/*
+ * biops.h -- C ABI of libbiops.so, the MI355X (gfx950) batch-invariant operator library.
+ *
+ * Every entry point takes raw device pointers, element strides and a hipStream_t (passed as
+ * void*), launches asynchronously on that stream and returns a status code (BIOPS_OK == 0).
+ * On failure biops_last_error() returns a message for the calling thread.  No entry point
+ * allocates device memory: scratch space (attention scores, MoE intermediates, work lists) is
+ * passed in by the caller, sized by the matching *_workspace_size() query.
+ *
+ * Batch invariance contract: for every entry point, the arithmetic that produces one output
+ * element (the K-reduction order and MFMA instruction of a GEMM, the reduction tree of a row
+ * reduction) depends only on the sizes of that element's own reduction (K, or the row length),
+ * the dtype and the weight-side sizes (N, K), never on M, the batch count or the position of
+ * the row inside the batch.
+ *
+ * Reference interfaces replaced (yiannisha/robotics-batch-invariant-ops, Python + Triton):
+ *   batch_invariant_ops/batch_invariant_ops.py  and  batch_invariant_ops/moe.py
+ * The reference has no native FFI; each function below replaces one of its Triton launch
+ * wrappers (L1) or Python composites (L2), cited per declaration.
+ */
+#ifndef BIOPS_H
+#define BIOPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (dtype arguments). */
+enum {
+  BIOPS_F32 = 0,
+  BIOPS_F16 = 1,
+  BIOPS_BF16 = 2,
+  BIOPS_BOOL = 3, /* attention masks only (1 byte, nonzero = keep) */
+};
+
+/* Status codes. */
+enum {
+  BIOPS_OK = 0,
+  BIOPS_ERR_ARG = 1,    /* invalid size / pointer / flag                           */
+  BIOPS_ERR_LAYOUT = 2, /* stride pattern the kernels do not take (copy it first)  */
+  BIOPS_ERR_DTYPE = 3,  /* unsupported element type                                */
+  BIOPS_ERR_HIP = 4,    /* HIP runtime error (launch failure, no device)           */
+  BIOPS_ERR_SIZE = 5,   /* workspace too small                                     */
+};
+
+/* Reduction operators for biops_reduce. */
+enum { BIOPS_REDUCE_MEAN = 0, BIOPS_REDUCE_L2 = 1 };
+
+/* Causal alignment for attention. */
+enum {
+  BIOPS_CAUSAL_NONE = 0,
+  BIOPS_CAUSAL_TOP_LEFT = 1,     /* key j visible from query i iff j <= i               */
+  BIOPS_CAUSAL_BOTTOM_RIGHT = 2, /* key j visible iff j <= i + (kv_len - q_len)         */
+};
+
+/* ---------------------------------------------------------------- library / device ---- */
+
+/* Library version string ("0.2.0-mi355x"). */
+const char* biops_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* biops_last_error(void);
+
+/* Number of compute units of the current HIP device (cached per device); <0 on error.
+ * Replaces get_compute_units() (batch_invariant_ops.py:232-253). */
+int biops_compute_units(void);
+
+/* ---------------------------------------------------------------------- GEMM / BMM ---- */
+
+/* C[M,N] = A[M,K] . B[K,N] (+ bias[N]), fp32 accumulation, one rounding to dtype at the end,
+ * bias added to the fp32 accumulator before that rounding.  Strides are in elements.
+ * Layout: sAk == 1 (rows of A contiguous in K); either sBk == 1 (B given as W^T, the
+ * nn.Linear case) or sBn == 1 (row-major B); sCn == 1.  bias may be NULL.
+ * Replaces matmul_persistent + matmul_kernel_persistent (batch_invariant_ops.py:60-139,
+ * 271-343) and the mm/addmm/linear shims (1600-1616). */
+int biops_gemm(int dtype, int64_t M, int64_t N, int64_t K,
+               const void* A, int64_t sAm, int64_t sAk,
+               const void* B, int64_t sBk, int64_t sBn,
+               const void* bias,
+               void* C, int64_t sCm, int64_t sCn,
+               void* stream);
+
+/* Batched GEMM over a two-level batch index b = b1*nb2 + b2 (b1 < nb1, b2 < nb2):
+ *   C[b] = A[b] . B[b]
+ * with operand X of batch b at X + b1*sX1 + (b2/gX)*sX2, gA = gC = 1 and gB = group
+ * (grouped-query attention maps gB query heads onto one key/value head; use 1 otherwise).
+ * Batch strides may be 0 (broadcast operands, e.g. the MoE token matrix).  Each batch element
+ * is an independent GEMM with the biops_gemm arithmetic.  Same layout rules as biops_gemm.
+ * Replaces bmm_persistent + bmm_kernel_persistent (batch_invariant_ops.py:142-229, 346-431). */
+int biops_bmm(int dtype, int64_t nb1, int64_t nb2, int64_t M, int64_t N, int64_t K,
+              const void* A, int64_t sA1, int64_t sA2, int64_t sAm, int64_t sAk,
+              const void* B, int64_t sB1, int64_t sB2, int64_t gB, int64_t sBk, int64_t sBn,
+              void* C, int64_t sC1, int64_t sC2, int64_t sCm, int64_t sCn,
+              void* stream);
+
+/* --------------------------------------------------------------- row reductions ---- */
+
+/* out[r, :] = softmax(in[r, :]) (log_softmax if is_log != 0) over `cols` contiguous elements
+ * per row, rows at stride ld_in / ld_out.  fp32 arithmetic; softmax of an all -inf row is 0.
+ * dtype_in / dtype_out in {F32, F16, BF16}.
+ * Replaces _softmax_kernel/softmax (batch_invariant_ops.py:1074-1145) and
+ * _log_softmax_kernel/log_softmax (974-1071). */
+int biops_softmax(int dtype_in, int dtype_out, int64_t rows, int64_t cols,
+                  const void* in, int64_t ld_in, void* out, int64_t ld_out,
+                  int is_log, void* stream);
+
+/* Reduction over N of the strided (M, N, K) view in[m*sM + n*sN + k*sK]:
+ *   MEAN: out = (sum_n x) / N       L2: out = sqrt(sum_n x*x)
+ * fp32 accumulation; out[m*K + k] in dtype_out.
+ * Replaces mean_kernel/mean_dim (batch_invariant_ops.py:1347-1482) and
+ * _vector_norm_kernel/linalg_vector_norm_batch_invariant (1485-1597). */
+int biops_reduce(int op, int dtype_in, int dtype_out, int64_t M, int64_t N, int64_t K,
+                 const void* in, int64_t sM, int64_t sN, int64_t sK,
+                 void* out, void* stream);
+
+/* ------------------------------------------------------------------- attention ---- */
+
+/* Workspace bytes biops_sdpa needs (the materialised score/probability matrices). */
+int64_t biops_sdpa_workspace_size(int dtype, int64_t batch, int64_t hq, int64_t lq, int64_t lk);
+
+/* Eager attention out = softmax(round(round(Q K^T) * scale) (+mask | causal)) V with the
+ * roundings of the reference composite, for Q[B,Hq,Lq,D], K[B,Hkv,Lk,D], V[B,Hkv,Lk,Dv],
+ * out[B,Hq,Lq,Dv] (strides given per dim, last dim contiguous; out contiguous).  Hq must be a
+ * multiple of Hkv (GQA: query head h reads key/value head h / (Hq/Hkv)).
+ * mask (may be NULL): dtype BOOL (nonzero = keep) or `dtype` (additive), indexed as
+ * mask[b*mB + h*mH + i*mI + j*mJ] (broadcast dims have stride 0).  causal: BIOPS_CAUSAL_*
+ * (TOP_LEFT is the reference's is_causal); mask and causal are exclusive.
+ * Fully masked rows give 0.
+ * Replaces scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1148-1213). */
+int biops_sdpa(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+               int64_t d, int64_t dv,
+               const void* q, int64_t sqB, int64_t sqH, int64_t sqL,
+               const void* k, int64_t skB, int64_t skH, int64_t skL,
+               const void* v, int64_t svB, int64_t svH, int64_t svL,
+               const void* mask, int mask_dtype, int64_t mB, int64_t mH, int64_t mI, int64_t mJ,
+               int causal, float scale,
+               void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Host-side planning for packed variable-length attention.  Given the host copies of the
+ * cumulative offsets (nseq+1 entries each, validated by the caller), writes the per-sequence
+ * work list used by biops_varlen_sdpa into `plan` (host int64 array of
+ * biops_varlen_plan_len(nseq) entries) and returns the workspace bytes needed, or <0 on a
+ * malformed offset list.  Empty query or key ranges are dropped (their rows stay zero). */
+int64_t biops_varlen_plan_len(int64_t nseq);
+int64_t biops_varlen_plan(int64_t nseq, const int64_t* cu_q, const int64_t* cu_kv,
+                          int64_t hq, int64_t dv, int dtype, int64_t* plan);
+
+/* Packed varlen attention for q[1,Tq,Hq,D], k[1,Tk,Hkv,D], v[1,Tk,Hkv,Dv], out[1,Tq,Hq,Dv]
+ * (token stride sX_t, head stride sX_h, last dim contiguous).  `dplan` is the device copy of
+ * the host plan above; the caller has zeroed `out` (rows of no sequence stay 0).
+ * causal: BIOPS_CAUSAL_NONE / TOP_LEFT / BOTTOM_RIGHT (for equal lengths both equal standard
+ * causal).  Each sequence is an independent problem: its bits do not depend on the others.
+ * Replaces varlen_scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1216-1344). */
+int biops_varlen_sdpa(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
+                      const void* q, int64_t sq_t, int64_t sq_h,
+                      const void* k, int64_t sk_t, int64_t sk_h,
+                      const void* v, int64_t sv_t, int64_t sv_h,
+                      void* out, int64_t so_t, int64_t so_h,
+                      const int64_t* dplan, const int64_t* hplan, int causal, float scale,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- MoE ---- */
+
+/* Workspace bytes for biops_moe. */
+int64_t biops_moe_workspace_size(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
+                                 int64_t inter);
+
+/* Deterministic top-k SwiGLU mixture of experts:
+ *   act[e,t,:]  = round(round(silu(round(x_t . gate_e^T))) * round(x_t . up_e^T))
+ *   y[e,t,:]    = round(act[e,t,:] . down_e^T)
+ *   out[t,:]    = sum over slots s = 0..k-1, left to right, each term round(y[sel[t,s],t,:] *
+ *                 round(w[t,s])) and each partial sum rounded to dtype
+ * x[T,D] (row stride sx), gate/up given as [E,I,D] views with strides (sgE, sgI, sgD) and
+ * (suE, suI, suD), down as [E,D,I] with (sdE, sdD, sdI); each needs its D (resp. I) stride or
+ * its I (resp. D) stride equal to 1.  weights[T,k] fp32/dtype (w_dtype), sel[T,k] int64.
+ * Expert indices outside [0,E) make the call write zeros for that token and set *bad_index
+ * (device int32, may be NULL) to 1.  out[T,D] contiguous.
+ * Replaces deterministic_token_choice_moe (moe.py:11-92). */
+int biops_moe(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,
+              int64_t top_k,
+              const void* x, int64_t sx,
+              const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+              const void* up, int64_t suE, int64_t suI, int64_t suD,
+              const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+              const void* weights, int w_dtype, const int64_t* sel,
+              void* out, int32_t* bad_index,
+              void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BIOPS_H */

@@ -1,0 +1,211 @@
+"""Float64 CPU restatement of the reference operators (test infrastructure only).
+
+Each function follows the cited lines of yiannisha/robotics-batch-invariant-ops:
+``batch_invariant_ops/batch_invariant_ops.py`` (BIO) and ``batch_invariant_ops/moe.py`` (MOE).
+Arithmetic is float64 with explicit roundings to the working dtype exactly where the reference
+materialises a tensor of that dtype (GEMM outputs, the scaled / masked scores, softmax outputs,
+the SwiGLU intermediates, the weighted routes and every partial slot sum).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+__all__ = [
+    "rnd",
+    "matmul",
+    "bmm",
+    "linear",
+    "softmax",
+    "log_softmax",
+    "mean_dim",
+    "mean_dims",
+    "vector_norm",
+    "sdpa",
+    "varlen_sdpa",
+    "moe",
+    "gemm_abs",
+    "gamma",
+]
+
+_INT_DTYPES = (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8)
+
+
+def rnd(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Round a float64 tensor to ``dtype`` (round to nearest even), returned as float64."""
+    return x.to(dtype).double()
+
+
+def gamma(k: int, dtype: torch.dtype = torch.float32) -> float:
+    """Higham's gamma_k = k u / (1 - k u) for the accumulation precision (fp32 here)."""
+    u = 2.0**-24
+    ku = k * u
+    return ku / (1.0 - ku) if ku < 1 else math.inf
+
+
+def gemm_abs(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|A| @ |B| in float64: scales the dot-product error bound of every output element."""
+    return a.double().abs() @ b.double().abs()
+
+
+# ---------------------------------------------------------------------------- GEMM ----
+def matmul(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A @ B (+ bias) rounded once to A's dtype; the bias joins the wide accumulator before
+    the rounding (BIO 113-139 accumulate + 134-137 bias epilogue, 271-343 wrapper)."""
+    out = a.double() @ b.double()
+    if bias is not None:
+        out = out + bias.double()
+    return out.to(a.dtype)
+
+
+def bmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Per-batch C[i] = A[i] @ B[i], one rounding (BIO 142-229, 346-431)."""
+    return (a.double() @ b.double()).to(a.dtype)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Leading dims flatten into GEMM rows; B = W^T (BIO 1608-1616)."""
+    flat = x.reshape(-1, x.shape[-1])
+    return matmul(flat, w.t(), bias).reshape(*x.shape[:-1], w.shape[0])
+
+
+# ---------------------------------------------------------------- row reductions ----
+def softmax(x: torch.Tensor, dim: int = -1, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """exp(x - max) / sum; a row whose max is -inf gives 0, not NaN (BIO 1093-1114)."""
+    x64 = x.double()
+    m = x64.amax(dim=dim, keepdim=True) if x64.numel() else x64
+    all_neg_inf = m == -math.inf
+    shifted = torch.where(all_neg_inf, torch.full_like(x64, -math.inf), x64 - m)
+    e = torch.exp(shifted)
+    s = e.sum(dim=dim, keepdim=True)
+    out = torch.where(s == 0, torch.zeros_like(e), e / s)
+    return out.to(dtype or x.dtype)
+
+
+def log_softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """x - max - log(sum exp(x - max)) (BIO 994-1034)."""
+    x64 = x.double()
+    m = x64.amax(dim=dim, keepdim=True)
+    lse = torch.log(torch.exp(x64 - m).sum(dim=dim, keepdim=True))
+    return (x64 - m - lse).to(x.dtype)
+
+
+def mean_dim(x: torch.Tensor, dim: int, keepdim: bool = False, dtype: torch.dtype | None = None):
+    """Mean over one dim; integer inputs produce fp32; the input is cast to the output dtype
+    first (BIO 1411-1427); the sum is exact here (the kernels accumulate in fp32)."""
+    if dtype is None:
+        dtype = torch.float32 if x.dtype in _INT_DTYPES else x.dtype
+    x = x.to(dtype)
+    return x.double().mean(dim=dim, keepdim=keepdim).to(dtype)
+
+
+def mean_dims(x: torch.Tensor, dims, keepdim: bool = False, dtype: torch.dtype | None = None):
+    """Mean over several dims (all when empty) in the input (or given) dtype."""
+    if dtype is not None:
+        x = x.to(dtype)
+    if not dims:
+        dims = list(range(x.ndim))
+    out_dtype = torch.float32 if x.dtype in _INT_DTYPES else x.dtype
+    return x.to(out_dtype).double().mean(dim=tuple(dims), keepdim=keepdim).to(out_dtype)
+
+
+def vector_norm(x: torch.Tensor, dim=None, keepdim: bool = False, dtype: torch.dtype | None = None):
+    """sqrt(sum x^2) with the output in the (optionally cast) input dtype (BIO 1525-1597)."""
+    if dtype is not None:
+        x = x.to(dtype)
+    dims = tuple(range(x.ndim)) if dim is None else ((dim,) if isinstance(dim, int) else tuple(dim))
+    out = torch.sqrt((x.double() ** 2).sum(dim=dims, keepdim=keepdim))
+    return out.to(x.dtype)
+
+
+# ---------------------------------------------------------------------- attention ----
+def _scalar_to_opmath(scale: float) -> float:
+    """Python scalars multiply low-precision tensors in fp32 (the tensor op's compute type)."""
+    return float(torch.tensor(scale, dtype=torch.float32))
+
+
+def sdpa(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False):
+    """Eager attention with the reference's roundings (BIO 1148-1213):
+    S = round(Q K^T); S = round(S * scale); causal top-left / bool mask -> -inf, additive mask
+    -> round(S + mask); P = softmax(S) in q.dtype; O = round(P V)."""
+    dt = q.dtype
+    if enable_gqa:
+        rep = q.shape[-3] // k.shape[-3]
+        k = k.repeat_interleave(rep, dim=-3)
+        v = v.repeat_interleave(rep, dim=-3)
+    d = q.shape[-1]
+    s = rnd(q.double() @ k.double().transpose(-1, -2), dt)
+    sc = _scalar_to_opmath(scale if scale is not None else 1.0 / math.sqrt(d))
+    s = rnd(s * sc, dt)
+    lq, lk = q.shape[-2], k.shape[-2]
+    if is_causal:
+        keep = torch.ones(lq, lk, dtype=torch.bool).tril()
+        s = s.masked_fill(~keep, -math.inf)
+    elif attn_mask is not None:
+        if attn_mask.dtype == torch.bool:
+            s = s.masked_fill(~attn_mask, -math.inf)
+        else:
+            res_dtype = torch.promote_types(dt, attn_mask.dtype)
+            s = rnd(s + attn_mask.double(), res_dtype)
+    p = softmax(s, dim=-1, dtype=dt).double()
+    return rnd(p @ v.double(), dt).to(dt)
+
+
+def varlen_sdpa(q, k, v, cu_q, cu_kv, *, is_causal=False, causal_type=None, scale=None):
+    """Packed varlen attention (BIO 1216-1344): each sequence alone; rows outside every
+    sequence and sequences with empty key ranges are zero; BottomRight causal keeps
+    j <= i + (kv - q), TopLeft / None keeps j <= i."""
+    cu_q = [int(x) for x in cu_q]
+    cu_kv = [int(x) for x in cu_kv]
+    out = torch.zeros((1, q.shape[1], q.shape[2], v.shape[3]), dtype=v.dtype)
+    name = getattr(causal_type, "name", None)
+    if name is None and causal_type is not None:
+        name = str(causal_type).rsplit(".", 1)[-1]
+    for q0, q1, k0, k1 in zip(cu_q[:-1], cu_q[1:], cu_kv[:-1], cu_kv[1:]):
+        ql, kl = q1 - q0, k1 - k0
+        if ql == 0 or kl == 0:
+            continue
+        qi = q[:, q0:q1].transpose(1, 2)
+        ki = k[:, k0:k1].transpose(1, 2)
+        vi = v[:, k0:k1].transpose(1, 2)
+        mask = None
+        causal = is_causal
+        if is_causal and ql != kl:
+            qi_idx = torch.arange(ql)[:, None]
+            ki_idx = torch.arange(kl)[None, :]
+            shift = kl - ql if name == "BottomRight" else 0
+            mask = ki_idx <= qi_idx + shift
+            causal = False
+        o = sdpa(qi, ki, vi, attn_mask=mask, is_causal=causal, scale=scale,
+                 enable_gqa=qi.shape[-3] != ki.shape[-3])
+        out[:, q0:q1] = o.transpose(1, 2)
+    return out
+
+
+# ---------------------------------------------------------------------------- MoE ----
+def moe(hidden, routing_weights, selected, gate, up, down):
+    """Dense top-k SwiGLU MoE with the reference's roundings (MOE 75-91):
+    g = round(x gate_e^T), u = round(x up_e^T), a = round(round(silu(g)) * u),
+    y = round(a down_e^T), route = round(y[sel] * round(w)), out = fixed left-to-right slot sum
+    with a rounding after every add."""
+    dt = hidden.dtype
+    x = hidden.double()
+    T, k = selected.shape
+    D = hidden.shape[1]
+    if T == 0:
+        return hidden.new_empty((0, D))
+    if k == 0:
+        return hidden.new_zeros((T, D))
+    g = rnd(torch.einsum("td,eid->eti", x, gate.double()), dt)
+    u = rnd(torch.einsum("td,eid->eti", x, up.double()), dt)
+    a = rnd(rnd(g / (1.0 + torch.exp(-g)), dt) * u, dt)
+    y = rnd(torch.einsum("eti,edi->etd", a, down.double()), dt)
+    w = rnd(routing_weights.double(), dt)
+    t_idx = torch.arange(T)
+    out = None
+    for s in range(k):
+        route = rnd(y[selected[:, s], t_idx] * w[:, s : s + 1], dt)
+        out = route if out is None else rnd(out + route, dt)
+    return out.to(dt)

@@ -1,0 +1,142 @@
+"""ctypes binding of libbiops.so, the gfx950 HIP kernel library behind every operator.
+
+The library is loaded on first use.  There is no fallback: if the shared object is missing or
+no ROCm GPU is visible, the first kernel call raises ``RuntimeError`` naming the problem.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import torch  # loads torch's HIP runtime first, so libbiops.so binds to the same instance
+
+_LIB_PATH = pathlib.Path(__file__).resolve().parent / "libbiops.so"
+
+F32, F16, BF16, BOOL = 0, 1, 2, 3
+REDUCE_MEAN, REDUCE_L2 = 0, 1
+CAUSAL_NONE, CAUSAL_TOP_LEFT, CAUSAL_BOTTOM_RIGHT = 0, 1, 2
+
+_STATUS = {
+    1: "invalid argument",
+    2: "unsupported layout",
+    3: "unsupported dtype",
+    4: "HIP runtime error",
+    5: "workspace too small",
+}
+
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: BOOL}
+
+_i = ctypes.c_int
+_l = ctypes.c_int64
+_p = ctypes.c_void_p
+_f = ctypes.c_float
+
+_SIGNATURES = {
+    "biops_version": (ctypes.c_char_p, []),
+    "biops_last_error": (ctypes.c_char_p, []),
+    "biops_compute_units": (_i, []),
+    "biops_gemm": (_i, [_i, _l, _l, _l, _p, _l, _l, _p, _l, _l, _p, _p, _l, _l, _p]),
+    "biops_bmm": (
+        _i,
+        [_i, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p],
+    ),
+    "biops_softmax": (_i, [_i, _i, _l, _l, _p, _l, _p, _l, _i, _p]),
+    "biops_reduce": (_i, [_i, _i, _i, _l, _l, _l, _p, _l, _l, _l, _p, _p]),
+    "biops_sdpa_workspace_size": (_l, [_i, _l, _l, _l, _l]),
+    "biops_sdpa": (
+        _i,
+        [_i, _l, _l, _l, _l, _l, _l, _l]
+        + [_p, _l, _l, _l] * 3
+        + [_p, _i, _l, _l, _l, _l, _i, _f, _p, _p, _l, _p],
+    ),
+    "biops_varlen_plan_len": (_l, [_l]),
+    "biops_varlen_plan": (_l, [_l, _p, _p, _l, _l, _i, _p]),
+    "biops_varlen_sdpa": (
+        _i,
+        [_i, _l, _l, _l, _l] + [_p, _l, _l] * 4 + [_p, _p, _i, _f, _p, _l, _p],
+    ),
+    "biops_moe_workspace_size": (_l, [_i, _l, _l, _l, _l]),
+    "biops_moe": (
+        _i,
+        [_i, _l, _l, _l, _l, _l, _p, _l]
+        + [_p, _l, _l, _l] * 3
+        + [_p, _i, _p, _p, _p, _p, _l, _p],
+    ),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def library_path() -> pathlib.Path:
+    return _LIB_PATH
+
+
+def load(require_gpu: bool = True) -> ctypes.CDLL:
+    """Load libbiops.so (once).  With ``require_gpu`` also insist on a visible ROCm GPU."""
+    global _lib
+    if require_gpu and not torch.cuda.is_available():
+        raise RuntimeError(
+            "batch_invariant_ops needs a ROCm GPU: torch.cuda.is_available() is False"
+        )
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not _LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{_LIB_PATH} is missing; build it with "
+                        "`python robotics-batch-invariant-ops_amd/build_lib.py`"
+                    )
+                lib = ctypes.CDLL(str(_LIB_PATH))
+                for name, (res, args) in _SIGNATURES.items():
+                    fn = getattr(lib, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = lib
+    return _lib
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"batch_invariant_ops kernels do not support {dtype}") from None
+
+
+def stream_of(tensor: torch.Tensor) -> int:
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load(require_gpu=False).biops_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({_STATUS.get(rc, rc)}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    check(getattr(lib, name)(*args), name)
+
+
+def require_gpu_tensors(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                f"batch_invariant_ops kernels run on ROCm GPU tensors, got device {t.device}"
+            )
+
+
+def lib_version() -> str:
+    return load(require_gpu=False).biops_version().decode()
+
+
+def env_flag(name: str, default: bool) -> bool:
+    value = os.environ.get(name)
+    if value is None:
+        return default
+    return value not in {"0", "false", "False", ""}

@@ -1,0 +1,91 @@
+"""Deterministic token-choice mixture of experts on the library's fixed-schedule kernels."""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+
+def _unit_stride_weight(w: torch.Tensor) -> torch.Tensor:
+    """[E, rows, K] expert weight with a unit stride in its rows or in K."""
+    return w if w.stride(1) == 1 or w.stride(2) == 1 else w.contiguous()
+
+
+def deterministic_token_choice_moe(
+    hidden_states: torch.Tensor,
+    routing_weights: torch.Tensor,
+    selected_experts: torch.Tensor,
+    gate_weight: torch.Tensor,
+    up_weight: torch.Tensor,
+    down_weight: torch.Tensor,
+    workspace: dict[str, torch.Tensor] | None = None,
+) -> torch.Tensor:
+    """Top-k SwiGLU MoE without atomic routing or accumulation.
+
+    Reference: deterministic_token_choice_moe (moe.py:11-92).  ``gate_weight`` and
+    ``up_weight`` have shape ``(E, I, D)`` and ``down_weight`` ``(E, D, I)``.  Every expert is
+    evaluated for every token with fixed-schedule GEMMs (gate and up in one launch with the
+    SwiGLU epilogue ``round(round(silu(round(g))) * round(u))``, then the down projection);
+    the selected routes are weighted by ``round(routing_weight)`` and summed over the top-k
+    slots left to right with a rounding after every add.  ``workspace`` is accepted for
+    drop-in compatibility and ignored, as in the reference.
+
+    Expert indices outside ``[0, E)`` raise ``RuntimeError`` after the kernels ran (the kernels
+    never read out of range); set ``BIOPS_MOE_CHECK_INDICES=0`` to skip that host check.
+    """
+    del workspace
+    if hidden_states.ndim != 2:
+        raise ValueError(f"hidden_states must have shape (tokens, hidden), got {hidden_states.shape}")
+    if routing_weights.ndim != 2 or selected_experts.shape != routing_weights.shape:
+        raise ValueError("routing_weights and selected_experts must have the same (tokens, top_k) shape")
+    if routing_weights.shape[0] != hidden_states.shape[0]:
+        raise ValueError("routing tensors and hidden_states have different token counts")
+    if gate_weight.ndim != 3 or up_weight.shape != gate_weight.shape:
+        raise ValueError("gate_weight and up_weight must have the same (experts, intermediate, hidden) shape")
+    num_experts, intermediate_size, hidden_size = gate_weight.shape
+    if hidden_states.shape[1] != hidden_size:
+        raise ValueError("hidden_states and expert weights have incompatible hidden dimensions")
+    if down_weight.shape != (num_experts, hidden_size, intermediate_size):
+        raise ValueError("down_weight must have shape (experts, hidden, intermediate)")
+    token_count, top_k = selected_experts.shape
+    if token_count == 0:
+        return hidden_states.new_empty((0, hidden_size))
+    if top_k == 0:
+        return hidden_states.new_zeros((token_count, hidden_size))
+    dtype = hidden_states.dtype
+    if gate_weight.dtype != dtype or up_weight.dtype != dtype or down_weight.dtype != dtype:
+        raise ValueError("hidden_states and expert weights must share one dtype")
+    nat.require_gpu_tensors(hidden_states, routing_weights, selected_experts, gate_weight, up_weight, down_weight)
+    code = nat.dtype_code(dtype)
+
+    x = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
+    gate = _unit_stride_weight(gate_weight)
+    up = _unit_stride_weight(up_weight)
+    if gate.stride() != up.stride():
+        gate, up = gate.contiguous(), up.contiguous()
+    down = _unit_stride_weight(down_weight)
+    # routing_weights.to(activation dtype), as the reference does before the multiply
+    weights = routing_weights.to(dtype).contiguous()
+    selected = selected_experts.to(torch.int64).contiguous()
+
+    out = torch.empty((token_count, hidden_size), dtype=dtype, device=x.device)
+    lib = nat.load()
+    ws_bytes = lib.biops_moe_workspace_size(code, token_count, num_experts, hidden_size, intermediate_size)
+    scratch = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=x.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=x.device)
+    nat.call(
+        "biops_moe",
+        code, token_count, num_experts, hidden_size, intermediate_size, top_k,
+        x.data_ptr(), x.stride(0),
+        gate.data_ptr(), *gate.stride(),
+        up.data_ptr(), *up.stride(),
+        down.data_ptr(), *down.stride(),
+        weights.data_ptr(), code, selected.data_ptr(),
+        out.data_ptr(), bad.data_ptr(),
+        scratch.data_ptr(), scratch.numel(),
+        nat.stream_of(out),
+    )
+    if nat.env_flag("BIOPS_MOE_CHECK_INDICES", True) and int(bad.item()) != 0:
+        raise RuntimeError("selected_experts contains an expert index outside [0, num_experts)")
+    return out

@@ -1,0 +1,64 @@
+// Host-side interface of the batched GEMM launcher shared by the GEMM, attention and MoE entry
+// points.
+#pragma once
+
+#include "gemm_core.h"
+
+namespace biops {
+
+enum { kEpiPlain = 0, kEpiBias = 1, kEpiSwiglu = 2 };
+
+// One launch covers nb1*nb2 independent GEMMs C[b] = A[b] . B[b] of equal shape.
+// Batch b = b1*nb2 + b2 addresses X + b1*sX1 + (b2/gX)*sX2 (gA = gC = 1, gB = args.gB).
+// B is K-major (column n at B + n*ldb, K contiguous) or N-major (K row k at B + k*ldb).
+// In SwiGLU mode B holds the gate weights and B2 the up weights (same layout and strides) and
+// N counts output columns (each needs one gate and one up column).
+struct BmmArgs {
+  const void* A;
+  const void* B;
+  const void* B2;
+  void* C;
+  const void* bias;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t nb1, nb2, gB;
+  int64_t sA1, sA2, sB1, sB2, sC1, sC2;
+  // filled by the launcher
+  int64_t tiles_m, tiles_n, total;
+  int32_t a_vec, b_vec;
+};
+
+int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream);
+
+// Packed variable-length attention work list (host and device copies share the layout):
+//   plan[0] items, plan[1] QK^T tiles, plan[2] PV tiles, plan[3] score rows,
+//   plan[4] score elements, plan[5..7] reserved,
+//   plan[8 + 8*i ..] = {q_start, q_len, kv_start, kv_len, s_off, qk_tile0, pv_tile0, row0}
+// for every sequence i with q_len > 0 and kv_len > 0.  The tile counts are for the fixed
+// varlen tile kVarlenBM x kVarlenBN; every head of a sequence is a separate GEMM problem.
+constexpr int kPlanHeader = 8;
+constexpr int kPlanStride = 8;
+constexpr int kVarlenBM = 128;
+constexpr int kVarlenBN = 128;
+
+enum { kGroupQK = 0, kGroupPV = 1 };
+
+// Score rows of a varlen sequence are stored at a pitch rounded up to 8 elements so that every
+// row starts 16-byte aligned (vector loads in the softmax and the PV GEMM).
+__host__ __device__ __forceinline__ int64_t varlen_score_ld(int64_t kv_len) { return (kv_len + 7) & ~int64_t(7); }
+
+// Grouped GEMM over the plan: QK mode S_i,h = Q_i,h . K_i,h'^T; PV mode O_i,h = P_i,h . V_i,h'
+// (h' = h / group).  Token strides s*_t and head strides s*_h are in elements.
+struct GroupedArgs {
+  const void* q; const void* k; const void* v; void* s; void* out;
+  const int64_t* plan;
+  int64_t items, total_tiles, heads, group, d, dv;
+  int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h;
+};
+
+int launch_grouped(int dtype, const GroupedArgs& a, int mode, hipStream_t stream);
+
+// Resolve the B operand layout from its (K, N) strides; false if neither is unit-stride.
+bool b_layout(int64_t K, int64_t N, int64_t sBk, int64_t sBn, bool& kmajor, int64_t& ldb);
+
+}  // namespace biops

@@ -1,0 +1,171 @@
+"""GEMM / linear / BMM on the GPU: bitwise batch invariance and parity with the oracle.
+
+Mirrors the reference's operator tests (test_batch_invariance.py:42-172) with inputs made on
+the CPU from seeded generators, so that the oracle sees the same values."""
+
+import pytest
+import torch
+
+import oracle
+from batch_invariant_ops import bmm_persistent, linear_batch_invariant, matmul_persistent
+
+from _tol import assert_bitwise, assert_first_sample_equal, assert_gemm_close
+
+pytestmark = pytest.mark.gpu
+DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def randn(*shape, seed, dtype=torch.float32, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float32) * scale).to(dtype)
+
+
+def gpu(*ts):
+    out = tuple(t.cuda() for t in ts)
+    return out if len(out) > 1 else out[0]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch_size", (2, 3, 5, 17))
+def test_mm_is_batch_invariant(dtype, batch_size):
+    x = gpu(randn(batch_size, 257, seed=1000 + batch_size, dtype=dtype))
+    w = gpu(randn(257, 129, seed=1100 + batch_size, dtype=dtype))
+    assert_first_sample_equal(matmul_persistent(x[:1], w), matmul_persistent(x, w))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mm_rows_do_not_depend_on_position(dtype):
+    """Row i computed alone equals row i inside the batch for every i (MFMA lane position)."""
+    x = gpu(randn(70, 300, seed=1200, dtype=dtype))
+    w = gpu(randn(300, 200, seed=1201, dtype=dtype))
+    full = matmul_persistent(x, w)
+    for i in (0, 1, 5, 31, 32, 33, 63, 64, 69):
+        assert_bitwise(matmul_persistent(x[i : i + 1], w), full[i : i + 1], f"row {i}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mm_matches_oracle(dtype):
+    a = randn(37, 257, seed=2000, dtype=dtype)
+    b = randn(257, 91, seed=2001, dtype=dtype)
+    out = matmul_persistent(*gpu(a, b))
+    assert_gemm_close(out, oracle.matmul(a, b), oracle.gemm_abs(a, b), 257)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ("b_rowmajor", "b_transposed"))
+@pytest.mark.parametrize("shape", ((300, 2048, 520), (129, 65, 96), (5, 1, 33), (64, 4096, 256)))
+def test_mm_layouts_match_oracle(dtype, layout, shape):
+    m, k, n = shape
+    a = randn(m, k, seed=2100 + m, dtype=dtype)
+    if layout == "b_rowmajor":
+        b = randn(k, n, seed=2200 + n, dtype=dtype)
+    else:
+        b = randn(n, k, seed=2200 + n, dtype=dtype).t()
+    out = matmul_persistent(*gpu(a, b))
+    assert_gemm_close(out, oracle.matmul(a, b), oracle.gemm_abs(a, b), k)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mm_empty_and_zero_k(dtype):
+    a = gpu(randn(4, 0, seed=1, dtype=dtype))
+    b = gpu(randn(0, 7, seed=2, dtype=dtype))
+    assert torch.equal(matmul_persistent(a, b), torch.zeros(4, 7, dtype=dtype, device="cuda"))
+    assert matmul_persistent(gpu(randn(0, 5, seed=3, dtype=dtype)), gpu(randn(5, 3, seed=4, dtype=dtype))).shape == (0, 3)
+    bias = gpu(randn(7, seed=5, dtype=dtype))
+    assert torch.equal(matmul_persistent(a, b, bias), bias.expand(4, 7))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch_size", (2, 5, 17))
+def test_rank3_linear_is_batch_invariant(dtype, batch_size):
+    x = gpu(randn(batch_size, 37, 257, seed=2500 + batch_size, dtype=dtype))
+    w = gpu(randn(91, 257, seed=2600 + batch_size, dtype=dtype))
+    bias = gpu(randn(91, seed=2650 + batch_size, dtype=dtype))
+    assert_first_sample_equal(linear_batch_invariant(x[:1], w, bias), linear_batch_invariant(x, w, bias))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_matches_oracle(dtype):
+    x = randn(3, 37, 257, seed=2700, dtype=dtype)
+    w = randn(91, 257, seed=2701, dtype=dtype)
+    bias = randn(91, seed=2702, dtype=dtype)
+    out = linear_batch_invariant(*gpu(x, w, bias))
+    absprod = oracle.gemm_abs(x.reshape(-1, 257), w.t()) + bias.double().abs()
+    assert_gemm_close(out.reshape(-1, 91), oracle.linear(x, w, bias).reshape(-1, 91), absprod, 257)
+
+
+def test_projector_linear_shape_is_batch_invariant():
+    x = gpu(randn(2, 256, 1024, seed=2750, dtype=torch.bfloat16))
+    w = gpu(randn(4096, 1024, seed=2751, dtype=torch.bfloat16))
+    bias = gpu(randn(4096, seed=2752, dtype=torch.bfloat16))
+    assert_first_sample_equal(linear_batch_invariant(x[:1], w, bias), linear_batch_invariant(x, w, bias))
+
+
+def test_small_batch_fp32_projection_is_batch_invariant():
+    x = gpu(randn(2, 2304, seed=2775))
+    w = gpu(randn(2304, 2304, seed=2776))
+    bias = gpu(randn(2304, seed=2777))
+    assert_first_sample_equal(linear_batch_invariant(x[:1], w, bias), linear_batch_invariant(x, w, bias))
+
+
+@pytest.mark.parametrize(("n", "k", "with_bias"), ((8192, 2048, True), (2048, 8192, False)))
+def test_metric_gemm_rows_identical_for_every_m(n, k, with_bias):
+    """The metric's M sweep: every row of an M-row GEMM equals the same row of the 4096-row GEMM."""
+    x = gpu(randn(4096, k, seed=2800 + n, dtype=torch.bfloat16))
+    w = gpu(randn(n, k, seed=2801 + n, dtype=torch.bfloat16, scale=0.02))
+    bias = gpu(randn(n, seed=2802 + n, dtype=torch.bfloat16, scale=0.02)) if with_bias else None
+    full = linear_batch_invariant(x, w, bias)
+    for m in (1, 2, 3, 4, 64, 100, 129, 256, 1024, 2048, 4095):
+        assert_bitwise(linear_batch_invariant(x[:m], w, bias), full[:m], f"M={m}")
+    # rows computed at an offset (the sample sits at a different tile position)
+    assert_bitwise(linear_batch_invariant(x[77:200], w, bias), full[77:200], "rows 77..199")
+
+
+def test_metric_gemm_matches_oracle():
+    x = randn(300, 2048, seed=2900, dtype=torch.bfloat16)
+    w = randn(8192, 2048, seed=2901, dtype=torch.bfloat16, scale=0.02)
+    bias = randn(8192, seed=2902, dtype=torch.bfloat16, scale=0.02)
+    out = linear_batch_invariant(*gpu(x, w, bias))
+    absprod = oracle.gemm_abs(x, w.t()) + bias.double().abs()
+    assert_gemm_close(out, oracle.linear(x, w, bias), absprod, 2048)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch_size", (2, 3, 5, 17))
+def test_bmm_is_batch_invariant(dtype, batch_size):
+    a = gpu(randn(batch_size, 33, 65, seed=3000 + batch_size, dtype=dtype))
+    b = gpu(randn(batch_size, 65, 47, seed=3100 + batch_size, dtype=dtype))
+    assert_first_sample_equal(bmm_persistent(a[:1], b[:1]), bmm_persistent(a, b))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bmm_matches_oracle_for_noncontiguous_attention_inputs(dtype):
+    q = randn(4, 8, 33, 65, seed=4000, dtype=dtype).reshape(-1, 33, 65)
+    k = randn(4, 8, 47, 65, seed=4001, dtype=dtype).reshape(-1, 47, 65).transpose(1, 2)
+    out = bmm_persistent(*gpu(q, k))
+    assert_gemm_close(out, oracle.bmm(q, k), q.double().abs() @ k.double().abs(), 65)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bmm_broadcast_operand_matches_oracle(dtype):
+    """Stride-0 batch operand (the MoE token matrix) and a row-major right operand."""
+    x = randn(19, 40, seed=4100, dtype=dtype)
+    w = randn(6, 40, 70, seed=4101, dtype=dtype)
+    a = x.unsqueeze(0).expand(6, -1, -1)
+    out = bmm_persistent(gpu(x).unsqueeze(0).expand(6, -1, -1), gpu(w))
+    assert_gemm_close(out, oracle.bmm(a, w), a.double().abs() @ w.double().abs(), 40)
+
+
+def test_bmm_supports_more_than_grid_limit():
+    a = gpu(randn(70_000, 1, 4, seed=4500, dtype=torch.bfloat16))
+    b = gpu(randn(70_000, 4, 1, seed=4501, dtype=torch.bfloat16))
+    full = bmm_persistent(a, b)
+    assert_first_sample_equal(bmm_persistent(a[:1], b[:1]), full)
+    ref = oracle.bmm(a.cpu(), b.cpu())
+    assert_gemm_close(full, ref, a.cpu().double().abs() @ b.cpu().double().abs(), 4)
+
+
+def test_bmm_empty():
+    a = gpu(randn(0, 3, 4, seed=1))
+    b = gpu(randn(0, 4, 5, seed=2))
+    assert bmm_persistent(a, b).shape == (0, 3, 5)

@@ -1,0 +1,117 @@
+"""Deterministic token-choice MoE on the GPU (reference tests test_batch_invariance.py:745-780).
+
+Parity bound: the MoE rounds gate, up, silu(gate), the SwiGLU product, the down projection, each
+weighted route and each partial slot sum.  Each of those roundings can differ by one ulp when the
+fp32 accumulations straddle a rounding boundary, so the bound is (4 + top_k) ulps of the output
+dtype relative to max|y| over the routes, plus the fp32 accumulation term.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from batch_invariant_ops import deterministic_token_choice_moe as moe
+
+from _tol import ULP, assert_bitwise, assert_close_scaled
+
+pytestmark = pytest.mark.gpu
+
+
+def randn(*shape, seed, dtype=torch.float32, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def routing(tokens, experts, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    selected = torch.stack([torch.randperm(experts, generator=g)[:k] for _ in range(tokens)])
+    weights = torch.rand(tokens, k, generator=g)
+    return weights, selected
+
+
+def test_moe_matches_route_by_route_loop():
+    """Brute-force route loop of the reference test (float32, test_batch_invariance.py:757-766)."""
+    hidden = randn(7, 12, seed=7400)
+    gate = randn(5, 16, 12, seed=7401)
+    up = randn(5, 16, 12, seed=7402)
+    down = randn(5, 12, 16, seed=7403)
+    g = torch.Generator().manual_seed(7404)
+    selected = torch.randint(0, 5, (7, 3), generator=g)
+    weights = torch.rand(7, 3, generator=g)
+    args = [t.cuda() for t in (hidden, weights, selected, gate, up, down)]
+    actual = moe(*args)
+    assert_bitwise(actual, moe(*args), "repeat call")
+    expected = torch.zeros(7, 12, dtype=torch.float64)
+    for t in range(7):
+        for s in range(3):
+            e = selected[t, s]
+            h = hidden[t].double()
+            inter = F.silu(gate[e].double() @ h) * (up[e].double() @ h)
+            expected[t] += (down[e].double() @ inter) * weights[t, s].double()
+    assert_close_scaled(actual, expected, rel=2e-5, abs_scale=2e-5, what="route loop")
+
+
+@pytest.mark.parametrize("dtype", (torch.float32, torch.bfloat16, torch.float16))
+def test_moe_matches_oracle(dtype):
+    T, E, D, I, k = 37, 6, 64, 80, 3
+    hidden = randn(T, D, seed=7410, dtype=dtype)
+    gate = randn(E, I, D, seed=7411, dtype=dtype, scale=0.2)
+    up = randn(E, I, D, seed=7412, dtype=dtype, scale=0.2)
+    down = randn(E, D, I, seed=7413, dtype=dtype, scale=0.2)
+    w, sel = routing(T, E, k, 7414)
+    out = moe(*(t.cuda() for t in (hidden, w, sel, gate, up, down)))
+    ref = oracle.moe(hidden, w, sel, gate, up, down)
+    scale = float(ref.double().abs().max())
+    n = 4 + k
+    assert_close_scaled(out, ref, rel=n * ULP[dtype], abs_scale=n * ULP[dtype] * scale, what="moe")
+
+
+def test_moe_is_batch_invariant():
+    hidden = randn(11, 64, seed=7425).cuda()
+    gate = randn(7, 80, 64, seed=7426).cuda()
+    up = randn(7, 80, 64, seed=7427).cuda()
+    down = randn(7, 64, 80, seed=7428).cuda()
+    g = torch.Generator().manual_seed(7429)
+    selected = torch.randint(0, 7, (11, 4), generator=g).cuda()
+    weights = torch.rand(11, 4, generator=g).cuda()
+    alone = moe(hidden[:1], weights[:1], selected[:1], gate, up, down)
+    together = moe(hidden, weights, selected, gate, up, down)
+    assert_bitwise(alone, together[:1], "token 0")
+    mid = moe(hidden[5:8], weights[5:8], selected[5:8], gate, up, down)
+    assert_bitwise(mid, together[5:8], "tokens 5..7")
+
+
+def test_moe_fused_gate_up_layout():
+    """gate/up given as transposed halves of a fused [E, D, 2I] tensor (N-major operands)."""
+    T, E, D, I, k = 9, 4, 48, 40, 2
+    hidden = randn(T, D, seed=7440, dtype=torch.bfloat16)
+    gu = randn(E, D, 2 * I, seed=7441, dtype=torch.bfloat16, scale=0.1)
+    dn = randn(E, I, D, seed=7442, dtype=torch.bfloat16, scale=0.1)
+    w, sel = routing(T, E, k, 7443)
+    gate, up, down = gu[..., :I].transpose(1, 2), gu[..., I:].transpose(1, 2), dn.transpose(1, 2)
+    out = moe(hidden.cuda(), w.cuda(), sel.cuda(), gate.cuda(), up.cuda(), down.cuda())
+    ref = oracle.moe(hidden, w, sel, gate, up, down)
+    contiguous = moe(hidden.cuda(), w.cuda(), sel.cuda(), gate.contiguous().cuda(), up.contiguous().cuda(),
+                     down.contiguous().cuda())
+    assert_bitwise(out, contiguous, "strided vs contiguous weights")
+    scale = float(ref.double().abs().max())
+    assert_close_scaled(out, ref, rel=6 * ULP[torch.bfloat16], abs_scale=6 * ULP[torch.bfloat16] * scale)
+
+
+def test_moe_edge_cases():
+    hidden = randn(3, 8, seed=7450).cuda()
+    gate = randn(2, 4, 8, seed=7451).cuda()
+    down = randn(2, 8, 4, seed=7452).cuda()
+    empty = moe(hidden[:0], torch.zeros(0, 2, device="cuda"), torch.zeros(0, 2, dtype=torch.int64, device="cuda"),
+                gate, gate, down)
+    assert empty.shape == (0, 8)
+    zero_k = moe(hidden, torch.zeros(3, 0, device="cuda"), torch.zeros(3, 0, dtype=torch.int64, device="cuda"),
+                 gate, gate, down)
+    assert torch.count_nonzero(zero_k) == 0 and zero_k.shape == (3, 8)
+    with pytest.raises(ValueError):
+        moe(hidden, torch.zeros(3, 2, device="cuda"), torch.zeros(3, 1, dtype=torch.int64, device="cuda"),
+            gate, gate, down)
+    with pytest.raises(RuntimeError, match="outside"):
+        moe(hidden, torch.ones(3, 1, device="cuda"), torch.full((3, 1), 5, dtype=torch.int64, device="cuda"),
+            gate, gate, down)
