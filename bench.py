@@ -1,0 +1,366 @@
+"""Benchmark of the batch-invariant bf16 GEMM path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs REPORT.json]
+
+Metric: bf16 batch-invariant GEMM TFLOP/s (% of MFMA peak), M = 1..4096, on
+configs[1]'s two linears (VLA action-expert stack): x[M,2048] -> W1[8192,2048] + b1, and
+h[M,8192] -> W2[2048,8192].  One step = one pass over M in {1, 2, 4, ..., 4096} of both
+linears through the library (linear_batch_invariant -> biops_gemm), inputs resident in HBM.
+value = sum of FLOPs / wall time of the step.  The line also carries the roofline of the
+dominant kernel (M = 4096, measured alone), the bitwise B=1-vs-B=N check and a CPU baseline.
+
+--configs REPORT.json additionally runs the five BASELINE configs (BI check + throughput of
+every kernel family) and writes them to REPORT.json; the headline line is unchanged.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "robotics-batch-invariant-ops_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+M_SWEEP = [2**i for i in range(13)]  # 1 .. 4096
+SHAPES = ((8192, 2048, True), (2048, 8192, False))  # (N, K, bias)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--configs", default=None, help="also run the 5 BASELINE configs, write a JSON report")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    return p.parse_args()
+
+
+def event_time(fn, iters, stream=None):
+    """Average milliseconds per call of fn() measured with HIP events on the launch stream."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def cpu_baseline(seconds):
+    """Stock PyTorch CPU F.linear in bf16 -- the reference's own CPU path for this op -- on a
+    bounded sample of the same workload (M = 256 rows, both linears), repeated for ~seconds."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(20)
+    m = 256
+    x = torch.randn(m, 2048, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(8192, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    b1 = (torch.randn(8192, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(torch.bfloat16)
+    h = torch.randn(m, 8192, generator=g).to(torch.bfloat16)
+    F.linear(x, w1, b1)
+    F.linear(h, w2)
+    flops = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds or reps < 2:
+        F.linear(x, w1, b1)
+        F.linear(h, w2)
+        flops += 2 * 2.0 * m * 8192 * 2048
+        reps += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"stock torch {torch.__version__} CPU F.linear bf16 (the reference's CPU path), "
+        f"M=256 rows of both configs[1] linears, {reps} reps in {dt:.1f}s",
+    }
+
+
+def _bitwise(a, b):
+    import torch
+
+    return bool(torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)))
+
+
+def run_all():
+    """The five BASELINE configs: bitwise batch invariance and per-kernel-family throughput."""
+    import torch
+    import torch.nn.functional as F
+
+    import batch_invariant_ops as bio
+    from batch_invariant_ops import _native as nat
+
+    dev = torch.device("cuda:0")
+    report = {}
+
+    # C1: README fp32 mm check
+    a = torch.linspace(-100, 100, 2048 * 4096, device=dev).reshape(2048, 4096)
+    b = torch.linspace(-100, 100, 4096 * 4096, device=dev).reshape(4096, 4096)
+    full = bio.matmul_persistent(a, b)
+    ms = event_time(lambda: bio.matmul_persistent(a, b), 10)
+    report["C1_fp32_mm"] = {
+        "bitwise_m1_vs_m2048": _bitwise(bio.matmul_persistent(a[:1], b), full[:1]),
+        "ms": ms,
+        "tflops": 2 * 2048 * 4096 * 4096 / (ms * 1e-3) / 1e12,
+        "frac_fp32_peak": 2 * 2048 * 4096 * 4096 / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+    }
+    del a, b, full
+
+    # C2: bf16 linear + RMSNorm stack, B in {1, 8, 32}
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(32, 256, 2048, generator=g).to(torch.bfloat16).to(dev)
+    g = torch.Generator().manual_seed(20)
+    w1 = (torch.randn(8192, 2048, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    b1 = (torch.randn(8192, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    rw = torch.ones(2048, dtype=torch.bfloat16, device=dev)
+
+    def stack(inp):
+        with bio.set_batch_invariant_mode():
+            h = F.linear(inp, w1, b1)
+            y = F.linear(h, w2)
+            var = y.float().pow(2).mean(-1, keepdim=True)
+            yn = (y.float() * torch.rsqrt(var + 1e-6)).to(torch.bfloat16) * rw
+            return yn, yn.mean(-1), torch.linalg.vector_norm(yn, dim=-1)
+
+    outs = {bsz: stack(x[:bsz]) for bsz in (1, 8, 32)}
+    c2_bi = all(_bitwise(outs[bsz][i], outs[32][i][:bsz]) for bsz in (1, 8) for i in range(3))
+    c2 = {"bitwise_per_sample_B1_B8_B32": c2_bi}
+    for bsz in (1, 8, 32):
+        xb = x[:bsz]
+        m = bsz * 256
+        ms = event_time(lambda: stack(xb), 10)
+        c2[f"B{bsz}_stack_ms"] = ms
+        c2[f"B{bsz}_gemm_tflops_effective"] = 2 * 2 * m * 8192 * 2048 / (ms * 1e-3) / 1e12
+    yb = outs[32][0]
+    ms_mean = event_time(lambda: bio.mean_dim(yb, -1), 50)
+    ms_norm = event_time(lambda: bio.linalg_vector_norm_batch_invariant(yb, dim=-1), 50)
+    nbytes = yb.numel() * 2 + yb.numel() // 2048 * 2
+    c2["mean_B32_GBs"] = nbytes / (ms_mean * 1e-3) / 1e9
+    c2["norm_B32_GBs"] = nbytes / (ms_norm * 1e-3) / 1e9
+    report["C2_linear_rmsnorm"] = c2
+    del x, w1, b1, w2, outs
+
+    # HBM-bound row kernels at larger sizes
+    big = torch.randn(16 * 16 * 1024, 1024, device=dev).to(torch.bfloat16)
+    ms_sm = event_time(lambda: bio.softmax(big, -1), 20)
+    vol = torch.randn(8, 1024, 4, 132, 160, device=dev).to(torch.bfloat16)
+    ms_vn = event_time(lambda: bio.linalg_vector_norm_batch_invariant(vol, dim=1), 10)
+    rows = torch.randn(65536, 2048, device=dev).to(torch.bfloat16)
+    ms_rn = event_time(lambda: bio.linalg_vector_norm_batch_invariant(rows, dim=-1), 20)
+    report["row_kernels"] = {
+        "softmax_262144x1024_bf16_GBs": 2 * big.numel() * 2 / (ms_sm * 1e-3) / 1e9,
+        "vector_norm_8x1024x4x132x160_dim1_bf16_GBs": (vol.numel() * 2 + vol.numel() // 1024 * 2) / (ms_vn * 1e-3) / 1e9,
+        "vector_norm_65536x2048_lastdim_bf16_GBs": (rows.numel() * 2 + 65536 * 2) / (ms_rn * 1e-3) / 1e9,
+    }
+    del big, vol, rows
+
+    # C3: SDPA prefill, GQA 16/4, B in {1, 4, 16}; causal and additive mask
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(16, 16, 1024, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).to(dev)
+    g = torch.Generator().manual_seed(30)
+    mask = (torch.rand(16, 1, 1024, 1024, generator=g) * -10)
+    mask[torch.rand(16, 1, 1024, 1024, generator=g) < 0.1] = -math.inf
+    mask = mask.to(torch.bfloat16).to(dev)
+    c3 = {}
+    for name, kw in (("causal", {"is_causal": True}), ("mask", {"attn_mask": mask})):
+        def run(bsz, kw=kw):
+            kk = dict(kw)
+            if "attn_mask" in kk:
+                kk["attn_mask"] = kk["attn_mask"][:bsz]
+            return bio.scaled_dot_product_attention_batch_invariant(q[:bsz], k[:bsz], v[:bsz], enable_gqa=True, **kk)
+
+        o16 = run(16)
+        c3[f"{name}_bitwise_B1_B4_B16"] = _bitwise(run(1), o16[:1]) and _bitwise(run(4), o16[:4])
+        ms = event_time(lambda: run(16), 5)
+        c3[f"{name}_B16_ms"] = ms
+        c3[f"{name}_B16_tflops_executed"] = 4 * 16 * 16 * 1024 * 1024 * 128 / (ms * 1e-3) / 1e12
+    report["C3_sdpa"] = c3
+    del q, k, v, mask
+
+    # C4: packed varlen, 32 sequences, bottom-right causal
+    g = torch.Generator().manual_seed(4)
+    lengths = torch.randint(64, 2049, (32,), generator=g)
+    total = int(lengths.sum())
+    q = torch.randn(1, total, 8, 64, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, total, 2, 64, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, total, 2, 64, generator=g).to(torch.bfloat16).to(dev)
+    cu = torch.zeros(33, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lengths, 0)
+    cu_d = cu.to(dev)
+    out = bio.varlen_scaled_dot_product_attention_batch_invariant(q, k, v, cu_d, cu_d, is_causal=True, causal_type="BottomRight")
+    bi = True
+    for s in (0, 7, 31):
+        s0, s1 = int(cu[s]), int(cu[s + 1])
+        one = torch.tensor([0, s1 - s0], dtype=torch.int32, device=dev)
+        alone = bio.varlen_scaled_dot_product_attention_batch_invariant(
+            q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], one, one, is_causal=True, causal_type="BottomRight")
+        bi &= _bitwise(alone, out[:, s0:s1])
+    ms = event_time(lambda: bio.varlen_scaled_dot_product_attention_batch_invariant(
+        q, k, v, cu_d, cu_d, is_causal=True, causal_type="BottomRight"), 5)
+    sumsq = float((lengths.double() ** 2).sum())
+    report["C4_varlen"] = {
+        "bitwise_seq_alone_vs_packed": bi,
+        "ms": ms,
+        "tflops_executed": 4 * 8 * 64 * sumsq / (ms * 1e-3) / 1e12,
+        "total_tokens": total,
+    }
+    del q, k, v
+
+    # C5: dense top-8 SwiGLU MoE, 64 experts
+    g = torch.Generator().manual_seed(5)
+    hidden = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
+    gu = (torch.randn(64, 2048, 1536, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    dn = (torch.randn(64, 768, 2048, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    logits = torch.randn(4096, 64, generator=g)
+    probs = torch.softmax(logits, -1)
+    wts, sel = torch.topk(probs, 8, dim=-1)
+    wts, sel = wts.to(dev), sel.to(dev)
+    gate, up, down = gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2), dn.transpose(1, 2)
+
+    def moe(t0, t1):
+        return bio.deterministic_token_choice_moe(hidden[t0:t1], wts[t0:t1], sel[t0:t1], gate, up, down)
+
+    full = moe(0, 4096)
+    c5 = {"bitwise_T1_T256_T4096": _bitwise(moe(0, 1), full[:1]) and _bitwise(moe(0, 256), full[:256])
+          and _bitwise(moe(256, 512), full[256:512])}
+    for t in (1, 256, 4096):
+        ms = event_time(lambda: moe(0, t), 3 if t == 4096 else 10)
+        c5[f"T{t}_ms"] = ms
+        c5[f"T{t}_dense_tflops"] = 6 * 64 * t * 2048 * 768 / (ms * 1e-3) / 1e12
+        c5[f"T{t}_weight_GBs"] = 64 * 3 * 2048 * 768 * 2 / (ms * 1e-3) / 1e9
+    report["C5_moe"] = c5
+    report["library"] = nat.lib_version()
+    return report
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on exactly one GPU (asked for {args.gpus}): this build's hot path is "
+            "single-GPU; see DESIGN.md for how it would shard.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    from batch_invariant_ops import linear_batch_invariant
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(20)
+    weights = {}
+    for n, k, has_bias in SHAPES:
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).to(dev) if has_bias else None
+        x = torch.randn(max(M_SWEEP), k, generator=g).to(torch.bfloat16).to(dev)
+        weights[(n, k)] = (x, w, b)
+
+    def step():
+        for m in M_SWEEP:
+            for n, k, _ in SHAPES:
+                x, w, b = weights[(n, k)]
+                linear_batch_invariant(x[:m], w, b)
+
+    step_flops = sum(2.0 * m * n * k for m in M_SWEEP for n, k, _ in SHAPES)
+
+    # bitwise batch invariance on the timed shapes (outside the timed region)
+    bitwise = True
+    for n, k, _ in SHAPES:
+        x, w, b = weights[(n, k)]
+        full = linear_batch_invariant(x, w, b)
+        for m in (1, 7, 256, 1024):
+            bitwise &= bool(torch.equal(linear_batch_invariant(x[:m], w, b), full[:m]))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = step_flops * args.steps / elapsed / 1e12
+
+    # per-M rates and the dominant kernel (largest M, first linear) timed alone with HIP events
+    sweep = {}
+    for m in M_SWEEP:
+        rates = []
+        for n, k, _ in SHAPES:
+            x, w, b = weights[(n, k)]
+            ms = event_time(lambda: linear_batch_invariant(x[:m], w, b), 10 if m >= 1024 else 30)
+            rates.append(2.0 * m * n * k / (ms * 1e-3) / 1e12)
+        sweep[str(m)] = [round(r, 2) for r in rates]
+    n0, k0, _ = SHAPES[0]
+    x, w, b = weights[(n0, k0)]
+    mmax = max(M_SWEEP)
+    kernel_ms = event_time(lambda: linear_batch_invariant(x, w, b), 50)
+    achieved = 2.0 * mmax * n0 * k0 / (kernel_ms * 1e-3) / 1e12
+    m_ge_1024 = [r for m in M_SWEEP if m >= 1024 for r in sweep[str(m)]]
+
+    line = {
+        "metric": "bf16 batch-invariant GEMM TFLOP/s (% MFMA peak) M=1..4096; bitwise B=1 vs B=N",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights)",
+        "config": {
+            "workload": "configs[1] linears 2048->8192(+bias) and 8192->2048, M in 1,2,4..4096, bf16",
+            "m_sweep": M_SWEEP,
+            "parallelism": "single GPU",
+        },
+        "bitwise_b1_vs_bn": bitwise,
+        "frac_peak_whole_sweep": round(value / PEAK_BF16_TFLOPS, 4),
+        "min_frac_peak_m_ge_1024": round(min(m_ge_1024) / PEAK_BF16_TFLOPS, 4),
+        "sweep_tflops_per_m": sweep,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": f"bmm_kernel<bf16> M={mmax} N={n0} K={k0} +bias",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "kernel_ms": round(kernel_ms, 5),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if args.configs:
+        report = run_all()
+        with open(args.configs, "w") as fh:
+            json.dump(report, fh, indent=1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+"""The drop-in boundary on the CPU: the C ABI library loads and exports every declared symbol,
+its host-side planning and validation paths behave, and the Python API mirrors the reference's
+surface, argument checks and mode bookkeeping (test_batch_invariance.py:783-792)."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import batch_invariant_ops as bio
+from batch_invariant_ops import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "biops.h")
+
+REFERENCE_API = {
+    "set_batch_invariant_mode", "is_batch_invariant_mode_enabled", "disable_batch_invariant_mode",
+    "enable_batch_invariant_mode", "matmul_persistent", "linear_batch_invariant", "bmm_persistent",
+    "conv1d_batch_invariant", "conv2d_batch_invariant", "conv3d_batch_invariant",
+    "conv_transpose2d_batch_invariant", "conv_transpose3d_batch_invariant",
+    "scaled_dot_product_attention_batch_invariant", "varlen_scaled_dot_product_attention_batch_invariant",
+    "linalg_vector_norm_batch_invariant", "softmax", "log_softmax", "mean_dim",
+    "get_batch_invariant_attention_block_size", "AttentionBlockSize", "deterministic_token_choice_moe",
+}
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(biops_\w+)\s*\(", text))
+
+
+def lib():
+    return nat.load(require_gpu=False)
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) >= 14
+    handle = ctypes.CDLL(str(nat.library_path()))
+    missing = [n for n in sorted(names) if not hasattr(handle, n)]
+    assert not missing, f"libbiops.so lacks {missing}"
+    assert names == set(nat.EXPORTED), "ctypes signatures and header disagree"
+
+
+def test_library_version():
+    assert lib().biops_version().decode() == "0.2.0-mi355x"
+
+
+def test_public_api_matches_reference_surface():
+    assert set(bio.__all__) == REFERENCE_API
+    assert bio.__version__ == "0.2.0"
+    assert bio.get_batch_invariant_attention_block_size() == bio.AttentionBlockSize(16, 16)
+    with pytest.raises(NotImplementedError):
+        bio.conv2d_batch_invariant(torch.zeros(1))
+
+
+def test_host_validation_needs_no_gpu():
+    L = lib()
+    null = None
+    # unsupported dtype, negative sizes, bad layouts are rejected before any launch
+    assert L.biops_gemm(9, 4, 4, 4, 16, 4, 1, 16, 4, 1, null, 16, 4, 1, null) == 3
+    assert L.biops_gemm(2, -1, 4, 4, 16, 4, 1, 16, 4, 1, null, 16, 4, 1, null) == 1
+    assert L.biops_gemm(2, 4, 4, 4, 16, 1, 4, 16, 4, 1, null, 16, 4, 1, null) == 2  # A not K-contiguous
+    assert L.biops_gemm(2, 4, 4, 4, 16, 4, 1, 16, 8, 8, null, 16, 4, 1, null) == 2  # B without unit stride
+    assert b"unit stride" in L.biops_last_error()
+    assert L.biops_gemm(2, 0, 4, 4, null, 4, 1, null, 4, 1, null, null, 4, 1, null) == 0  # empty
+    assert L.biops_bmm(2, 1, 6, 4, 4, 4, 16, 0, 0, 4, 1, 16, 0, 0, 4, 1, 4, 16, 0, 0, 4, 1, null) == 1  # group !| heads
+    assert L.biops_softmax(2, 7, 4, 4, 16, 4, 16, 4, 0, null) == 3
+    assert L.biops_reduce(5, 2, 2, 1, 1, 1, 16, 1, 1, 1, 16, null) == 1
+    assert L.biops_reduce(0, 2, 2, 4, 8, 1, 16, 8, 2, 1, 16, null) == 2  # strided rows with K == 1
+
+
+def test_workspace_queries():
+    L = lib()
+    assert L.biops_sdpa_workspace_size(2, 16, 16, 1024, 1024) == 16 * 16 * 1024 * 1024 * 2
+    assert L.biops_sdpa_workspace_size(0, 1, 1, 3, 5) == 3 * 8 * 4  # rows padded to 8 elements
+    assert L.biops_moe_workspace_size(2, 4096, 64, 2048, 768) == (64 * 4096 * 768 + 64 * 4096 * 2048) * 2
+    assert L.biops_moe_workspace_size(9, 1, 1, 1, 1) == -1
+
+
+def plan(cu_q, cu_kv, hq=4, dv=24, dtype=nat.BF16):
+    L = lib()
+    n = len(cu_q) - 1
+    out = np.zeros(L.biops_varlen_plan_len(n), dtype=np.int64)
+    q = np.asarray(cu_q, dtype=np.int64)
+    k = np.asarray(cu_kv, dtype=np.int64)
+    ws = L.biops_varlen_plan(n, q.ctypes.data, k.ctypes.data, hq, dv, dtype, out.ctypes.data)
+    return ws, out
+
+
+def test_varlen_plan_work_list():
+    # sequences: (q 5, kv 7), (q 0, kv 4) dropped, (q 300, kv 0) dropped, (q 130, kv 129)
+    ws, p = plan([0, 5, 5, 305, 435], [0, 7, 11, 11, 140], hq=4, dv=24)
+    items, qk_tiles, pv_tiles, rows, selems = p[:5]
+    assert items == 2
+    first = p[8:16].tolist()
+    second = p[16:24].tolist()
+    assert first == [0, 5, 0, 7, 0, 0, 0, 0]
+    # second item starts after 4 heads x 5 rows x pitch 8 of the first
+    assert second[:5] == [305, 130, 11, 129, 4 * 5 * 8]
+    assert second[5:] == [4 * 1 * 1, 4 * 1 * 1, 4 * 5]
+    assert qk_tiles == 4 + 4 * 2 * 2 and pv_tiles == 4 + 4 * 2 * 1
+    assert rows == 4 * 5 + 4 * 130
+    assert selems == 4 * 5 * 8 + 4 * 130 * 136
+    assert ws == selems * 2
+
+
+def test_varlen_plan_rejects_decreasing_offsets():
+    ws, _ = plan([0, 5, 3], [0, 2, 4])
+    assert ws < 0 and b"nondecreasing" in lib().biops_last_error()
+
+
+def test_ops_reject_cpu_tensors_and_bad_arguments():
+    x = torch.randn(3, 4)
+    with pytest.raises(AssertionError):
+        bio.matmul_persistent(x, torch.randn(5, 2))
+    with pytest.raises(AssertionError):
+        bio.bmm_persistent(x, x)
+    with pytest.raises(ValueError):
+        bio.matmul_persistent(x, torch.randn(4, 2))  # CPU tensors: no CPU path
+    with pytest.raises(ValueError):
+        bio.softmax(torch.ones(2, dtype=torch.int64))
+    with pytest.raises(ValueError):
+        bio.softmax(x, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        bio.scaled_dot_product_attention_batch_invariant(x[None], x[None], x[None], dropout_p=0.5)
+    with pytest.raises(ValueError):
+        bio.scaled_dot_product_attention_batch_invariant(x[None], x[None].double(), x[None])
+    with pytest.raises(ValueError):
+        bio.scaled_dot_product_attention_batch_invariant(x[None, None], x[None, None], x[None, None], enable_gqa=True,
+                                                         attn_mask=torch.ones(3, 3, dtype=torch.bool), is_causal=True)
+    with pytest.raises(ValueError):
+        bio.varlen_scaled_dot_product_attention_batch_invariant(x, x, x, torch.tensor([0, 3]), torch.tensor([0, 3]))
+    q = torch.zeros(1, 4, 2, 8)
+    with pytest.raises(ValueError):
+        bio.varlen_scaled_dot_product_attention_batch_invariant(q, q, q, torch.tensor([0.0, 4.0]), torch.tensor([0, 4]))
+    with pytest.raises(ValueError):
+        bio.varlen_scaled_dot_product_attention_batch_invariant(q, q, q, torch.tensor([1, 4]), torch.tensor([0, 4]))
+    with pytest.raises(ValueError):
+        bio.deterministic_token_choice_moe(x, torch.ones(3, 2), torch.zeros(3, 1, dtype=torch.long),
+                                           torch.ones(2, 5, 4), torch.ones(2, 5, 4), torch.ones(2, 4, 5))
+    with pytest.raises(ValueError):
+        bio.deterministic_token_choice_moe(x, torch.ones(3, 1), torch.zeros(3, 1, dtype=torch.long),
+                                           torch.ones(2, 5, 4), torch.ones(2, 5, 4), torch.ones(2, 5, 4))
+    with pytest.raises(AssertionError):
+        bio.linalg_vector_norm_batch_invariant(x)  # reference asserts a CUDA tensor
+
+
+def test_mode_context_is_exception_safe_and_reentrant():
+    assert not bio.is_batch_invariant_mode_enabled()
+    with pytest.raises(RuntimeError, match="sentinel"):
+        with bio.set_batch_invariant_mode():
+            assert bio.is_batch_invariant_mode_enabled()
+            with bio.set_batch_invariant_mode():
+                assert bio.is_batch_invariant_mode_enabled()
+            with bio.set_batch_invariant_mode(False):
+                assert not bio.is_batch_invariant_mode_enabled()
+            assert bio.is_batch_invariant_mode_enabled()
+            raise RuntimeError("sentinel")
+    assert not bio.is_batch_invariant_mode_enabled()
+    bio.enable_batch_invariant_mode()
+    bio.enable_batch_invariant_mode()  # idempotent
+    assert bio.is_batch_invariant_mode_enabled()
+    bio.disable_batch_invariant_mode()
+    assert not bio.is_batch_invariant_mode_enabled()
+
+
+def test_mode_registers_gpu_key_only():
+    """The overrides live on dispatch key CUDA (ROCm GPUs); CPU tensors keep the stock kernels."""
+    a = torch.randn(4, 5)
+    b = torch.randn(5, 3)
+    with bio.set_batch_invariant_mode():
+        assert torch.equal(torch.mm(a, b), a @ b)
+        assert torch.softmax(a, -1).shape == (4, 5)
+        assert a.mean(-1).shape == (4,)
+    names = [op for op, _ in bio.batch_invariant_ops._OVERRIDES]
+    assert names == [
+        "aten::mm", "aten::addmm", "aten::linear", "aten::bmm", "aten::scaled_dot_product_attention",
+        "aten::_softmax", "aten::_log_softmax", "aten::mean.dim", "aten::linalg_vector_norm",
+    ]
+    assert bio.batch_invariant_ops._DISPATCH_KEY == "CUDA"
+
+
+def test_missing_gpu_is_a_loud_error():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nat.load(require_gpu=True)
