@@ -95,6 +95,18 @@ int biops_bmm(int dtype, int64_t nb1, int64_t nb2, int64_t M, int64_t N, int64_t
               void* C, int64_t sC1, int64_t sC2, int64_t sCm, int64_t sCn,
               void* stream);
 
+/* Number of entries in the GEMM tile menu.  Each entry is a (block tile, wavefront layout, LDS
+ * ring depth) scheduling choice; all entries compute every output element with the same MFMA
+ * sequence, so they produce identical bits and differ in speed only.  No reference
+ * counterpart (the reference fixes one Triton config per dtype, batch_invariant_ops.py:294-319). */
+int biops_gemm_tile_count(void);
+
+/* Force GEMM tile entry `cfg` for every later GEMM/BMM launch in the process (-1 restores the
+ * automatic choice, which is the default; the BIOPS_GEMM_CFG environment variable sets the
+ * initial value).  Entries 0 and 7 have no fp32 kernel and fall back to the automatic choice
+ * for fp32.  For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
+int biops_set_gemm_tile(int cfg);
+
 /* --------------------------------------------------------------- row reductions ---- */
 
 /* out[r, :] = softmax(in[r, :]) (log_softmax if is_log != 0) over `cols` contiguous elements

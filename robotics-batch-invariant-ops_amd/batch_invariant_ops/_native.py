@@ -43,6 +43,8 @@ _SIGNATURES = {
         _i,
         [_i, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p],
     ),
+    "biops_gemm_tile_count": (_i, []),
+    "biops_set_gemm_tile": (_i, [_i]),
     "biops_softmax": (_i, [_i, _i, _l, _l, _p, _l, _p, _l, _i, _p]),
     "biops_reduce": (_i, [_i, _i, _i, _l, _l, _l, _p, _l, _l, _l, _p, _p]),
     "biops_sdpa_workspace_size": (_l, [_i, _l, _l, _l, _l]),

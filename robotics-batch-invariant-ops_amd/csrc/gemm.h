@@ -25,7 +25,7 @@ struct BmmArgs {
   int64_t sA1, sA2, sB1, sB2, sC1, sC2;
   // filled by the launcher
   int64_t tiles_m, tiles_n, total;
-  int32_t a_vec, b_vec;
+  int32_t a_vec, b_vec, c_vec;
 };
 
 int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream);

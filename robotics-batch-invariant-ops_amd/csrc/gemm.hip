@@ -1,33 +1,73 @@
 // Persistent fixed-schedule GEMM / batched GEMM entry points.
+#include <stdlib.h>
+
+#include <atomic>
+
 #include "gemm.h"
 
 namespace biops {
 
+// ------------------------------------------------------------------ tile menu ----
+// Every entry computes each output element with the same MFMA sequence (see gemm_core.h); the
+// entries differ in block tile, wavefront layout and LDS ring depth only.
+template <int ID> struct Cfg;
+#define BIOPS_CFG(ID, BM_, BN_, WGM_, WGN_, ST_, PERCU_)                             \
+  template <> struct Cfg<ID> {                                                    \
+    static constexpr int bm = BM_, bn = BN_, wgm = WGM_, wgn = WGN_, stages = ST_;   \
+    static constexpr int threads = 64 * WGM_ * WGN_, per_cu = PERCU_;             \
+    static constexpr int waves_per_eu = (WGM_ * WGN_ * PERCU_ + 3) / 4;           \
+  };
+//         id   BM   BN  WGM WGN stages  workgroups/CU
+BIOPS_CFG(0, 256, 256, 2, 2, 2, 1)
+BIOPS_CFG(1, 256, 128, 2, 2, 3, 1)
+BIOPS_CFG(2, 128, 128, 2, 2, 2, 2)
+BIOPS_CFG(3, 128, 64, 2, 2, 4, 1)
+BIOPS_CFG(4, 64, 64, 2, 2, 4, 2)
+BIOPS_CFG(5, 32, 64, 1, 2, 8, 1)
+BIOPS_CFG(6, 32, 32, 1, 1, 8, 1)
+BIOPS_CFG(7, 256, 256, 2, 4, 2, 1)
+#undef BIOPS_CFG
+constexpr int kNumCfg = 8;
+
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
-// Epilogues: plain C = round(acc); bias C = round(acc + bias[n]) (bias added in fp32 before the
-// single rounding); SwiGLU C = round(round(silu(round(g))) * round(u)) -- the roundings of
-// F.silu(gate) * up applied to rounded bmm outputs -- where gate and up accumulators of one
-// output sit in adjacent 32-column MFMA blocks of the same wavefront.
-template <typename T, int BM, int BN, bool BKM, int EPI>
-__global__ __launch_bounds__(kGemmThreads) void bmm_kernel(BmmArgs args) {
-  using Tile = GemmTile<T, BM, BN, BKM>;
-  __shared__ __attribute__((aligned(16))) char smem[Tile::LDS_BYTES];
+// Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
+// SwiGLU C = round(round(silu(round(g))) * round(u)) -- the roundings of F.silu(gate) * up
+// applied to rounded bmm outputs -- where gate and up accumulators of one output sit in
+// adjacent 32-column MFMA blocks of the same wavefront.
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
+__global__ __launch_bounds__(Cfg<CFG>::threads)
+__attribute__((amdgpu_waves_per_eu(Cfg<CFG>::waves_per_eu, Cfg<CFG>::waves_per_eu)))
+void bmm_kernel(BmmArgs args) {
+  using C = Cfg<CFG>;
+  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
+  constexpr int BM = C::bm, BN = C::bn;
+  constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
+  __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
   f32x16_t acc[Tile::FM][Tile::FN];
 
-  const int64_t G = gridDim.x;
-  const int64_t slot = xcd_slot(blockIdx.x, G);
-  constexpr int64_t kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
-  const int64_t tpb = args.tiles_m * args.tiles_n;
-  for (int64_t t = slot; t < args.total; t += G) {
-    const int64_t b = t / tpb;
-    int64_t tm, tn;
-    tile_coords(t - b * tpb, args.tiles_m, args.tiles_n, tm, tn);
-    const int64_t b1 = b / args.nb2;
-    const int64_t b2 = b - b1 * args.nb2;
-    const int64_t m0 = tm * BM, n0 = tn * kCols;
+  // Tile indices stay 32-bit (the launcher guarantees fewer than 2^31 tiles).
+  const uint32_t G = gridDim.x;
+  const uint32_t total = (uint32_t)args.total;
+  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
+  const uint32_t tpb = tiles_m * tiles_n;
+  const uint32_t nb2 = (uint32_t)args.nb2, gB = (uint32_t)args.gB;
+  for (uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G); t < total; t += G) {
+    const uint32_t b = t / tpb;
+    const uint32_t in_b = t - b * tpb;
+    // grouped order: 8 tile-rows form a group walked column by column
+    const uint32_t per_group = 8u * tiles_n;
+    const uint32_t group = in_b / per_group;
+    const uint32_t first = group * 8u;
+    const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
+    const uint32_t in_group = in_b - group * per_group;
+    const uint32_t tn = in_group / gsize;
+    const uint32_t tm = first + (in_group - tn * gsize);
+    const uint32_t b1 = b / nb2;
+    const uint32_t b2 = b - b1 * nb2;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * kCols;
 
     const T* A = reinterpret_cast<const T*>(args.A) + b1 * args.sA1 + b2 * args.sA2 + m0 * args.lda;
-    const int64_t boff = b1 * args.sB1 + (b2 / args.gB) * args.sB2 + (BKM ? n0 * args.ldb : n0);
+    const int64_t boff = b1 * args.sB1 + (b2 / gB) * args.sB2 + (BKM ? n0 * args.ldb : n0);
     BSource<T> src;
     src.p0 = reinterpret_cast<const T*>(args.B) + boff;
     src.p1 = EPI == kEpiSwiglu ? reinterpret_cast<const T*>(args.B2) + boff : src.p0;
@@ -40,94 +80,102 @@ __global__ __launch_bounds__(kGemmThreads) void bmm_kernel(BmmArgs args) {
 
     Tile::mainloop(smem, acc, A, args.lda, rows, args.a_vec != 0, src, args.K);
 
-    T* C = reinterpret_cast<T*>(args.C) + b1 * args.sC1 + b2 * args.sC2 + m0 * args.ldc + n0;
-    if constexpr (EPI == kEpiSwiglu) {
-#pragma unroll
-      for (int i = 0; i < Tile::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < Tile::FN; j += 2) {
-          const int c = Tile::acc_col(j);              // gate column in tile space
-          const int col = ((c >> 6) << 5) + (c & 31);  // output column
-          if (col >= cols) continue;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = Tile::acc_row(i, r);
-            if (row < rows) {
-              const float g = Num<T>::round(acc[i][j][r]);
-              const float u = Num<T>::round(acc[i][j + 1][r]);
-              const float s = Num<T>::round(g / (1.0f + expf(-g)));
-              Num<T>::store(C + (int64_t)row * args.ldc + col, s * u);
-            }
-          }
-        }
-    } else {
-      const T* bias = reinterpret_cast<const T*>(args.bias) + n0;
-#pragma unroll
-      for (int i = 0; i < Tile::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < Tile::FN; ++j) {
-          const int col = Tile::acc_col(j);
-          if (col >= cols) continue;
-          const float bv = EPI == kEpiBias ? Num<T>::load(bias + col) : 0.f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = Tile::acc_row(i, r);
-            if (row < rows) {
-              float v = acc[i][j][r];
-              if (EPI == kEpiBias) v += bv;
-              Num<T>::store(C + (int64_t)row * args.ldc + col, v);
-            }
-          }
-        }
-    }
-    // The next tile's prologue rewrites LDS stage 0: every wavefront finished reading LDS in
-    // the last main-loop iteration, which ended with a barrier.
+    T* Cp = reinterpret_cast<T*>(args.C) + b1 * args.sC1 + b2 * args.sC2 + m0 * args.ldc + n0;
+    const T* bias = (EPI != kEpiSwiglu && args.bias) ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
+    Tile::template epilogue<EPI == kEpiSwiglu>(smem, acc, Cp, args.ldc, rows < BM ? (int)rows : BM,
+                                               cols < kCols ? (int)cols : kCols, bias, args.c_vec != 0);
   }
 }
 
 // -------------------------------------------------------------- tile selection ----
-// The block tile depends only on (dtype, N, K) and the epilogue, never on M or the batch.
-struct TileChoice { int bm, bn; };
+// Measured full-chip throughput of each entry on large bf16 problems (TFLOP/s, MI355X), used
+// to estimate which entry finishes a problem first: a problem of T tiles on S = CUs x
+// (workgroups per CU) slots takes ceil(T / S) rounds of one tile time, and one tile time is
+// proportional to BM x BN x (workgroups per CU) / throughput.
+static const double kCfgRate[kNumCfg] = {520, 700, 830, 475, 500, 185, 108, 900};
+static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 256};
+static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 256};
+static const int kCfgPerCu[kNumCfg] = {1, 1, 2, 1, 2, 1, 1, 1};
 
-static TileChoice choose_tile(int dtype, int64_t N, int64_t K, int epi) {
-  (void)dtype; (void)N; (void)K; (void)epi;
-  return {128, 128};
+// Forced tile entry (-1: automatic).  Initialised from BIOPS_GEMM_CFG, settable through
+// biops_set_gemm_tile; every entry yields the same bits, so forcing one only changes speed.
+static std::atomic<int> g_forced_cfg{-2};
+
+static int forced_cfg() {
+  int v = g_forced_cfg.load(std::memory_order_relaxed);
+  if (v == -2) {
+    const char* e = getenv("BIOPS_GEMM_CFG");
+    v = e ? atoi(e) : -1;
+    int expected = -2;
+    g_forced_cfg.compare_exchange_strong(expected, v);
+    v = g_forced_cfg.load(std::memory_order_relaxed);
+  }
+  return v;
 }
 
-template <typename T, int BM, int BN, bool BKM, int EPI>
+static int pick_cfg(int dtype, const BmmArgs& a, int epi) {
+  if (epi == kEpiSwiglu) return 2;
+  const int forced = forced_cfg();
+  if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7)))
+    return forced;
+  const int cus = device_cus();
+  const int64_t batch = a.nb1 * a.nb2;
+  int best = 2;
+  double best_cost = 1e300;
+  for (int c = 0; c < kNumCfg; ++c) {
+    if (dtype == BIOPS_F32 && (c == 0 || c == 7)) continue;  // fp32 accumulators need the smaller tiles
+    const int64_t tiles = batch * cdiv(a.M, kCfgBM[c]) * cdiv(a.N, kCfgBN[c]);
+    const int64_t slots = (int64_t)cus * kCfgPerCu[c];
+    const double rounds = (double)cdiv(tiles, slots);
+    const double cost = rounds * (double)kCfgBM[c] * kCfgBN[c] * kCfgPerCu[c] / kCfgRate[c];
+    if (cost < best_cost) { best_cost = cost; best = c; }
+  }
+  return best;
+}
+
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
 static int launch_cfg(const BmmArgs& a0, hipStream_t stream) {
-  using Tile = GemmTile<T, BM, BN, BKM>;
+  using C = Cfg<CFG>;
   BmmArgs a = a0;
-  constexpr int64_t kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
-  a.tiles_m = cdiv(a.M, BM);
+  constexpr int64_t kCols = EPI == kEpiSwiglu ? C::bn / 2 : C::bn;
+  a.tiles_m = cdiv(a.M, C::bm);
   a.tiles_n = cdiv(a.N, kCols);
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
+  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int cus = device_cus();
   if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
-  const int per_cu = Tile::LDS_BYTES * 2 <= 160 * 1024 ? 2 : 1;
-  int64_t grid = (int64_t)cus * per_cu;
+  int64_t grid = (int64_t)cus * C::per_cu;
   if (a.total < grid) grid = a.total;
-  hipLaunchKernelGGL((bmm_kernel<T, BM, BN, BKM, EPI>), dim3((unsigned)grid), dim3(kGemmThreads),
+  hipLaunchKernelGGL((bmm_kernel<T, CFG, BKM, DIRECT, EPI>), dim3((unsigned)grid), dim3(C::threads),
                      0, stream, a);
   return check_launch("bmm_kernel");
 }
 
-template <typename T, int EPI>
-static int launch_typed(const BmmArgs& a, bool b_kmajor, TileChoice tc, hipStream_t stream) {
-  if (tc.bm == 128 && tc.bn == 128)
-    return b_kmajor ? launch_cfg<T, 128, 128, true, EPI>(a, stream)
-                    : launch_cfg<T, 128, 128, false, EPI>(a, stream);
-  return fail(BIOPS_ERR_ARG, "no kernel for tile %dx%d", tc.bm, tc.bn);
+template <typename T, int CFG, int EPI>
+static int launch_layout(const BmmArgs& a, bool b_kmajor, bool direct, hipStream_t s) {
+  if (!b_kmajor) return launch_cfg<T, CFG, false, false, EPI>(a, s);
+  if (direct) return launch_cfg<T, CFG, true, true, EPI>(a, s);
+  return launch_cfg<T, CFG, true, false, EPI>(a, s);
 }
 
-template <int EPI>
-static int launch_epi(int dtype, const BmmArgs& a, bool b_kmajor, TileChoice tc, hipStream_t s) {
-  switch (dtype) {
-    case BIOPS_F32: return launch_typed<float, EPI>(a, b_kmajor, tc, s);
-    case BIOPS_F16: return launch_typed<f16_t, EPI>(a, b_kmajor, tc, s);
-    case BIOPS_BF16: return launch_typed<bf16_t, EPI>(a, b_kmajor, tc, s);
-    default: return fail(BIOPS_ERR_DTYPE, "unsupported GEMM dtype %d", dtype);
+template <typename T, int EPI>
+static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, hipStream_t s) {
+  if constexpr (EPI == kEpiSwiglu) {
+    return launch_layout<T, 2, EPI>(a, b_kmajor, direct, s);
+  } else {
+    switch (cfg) {
+      case 0: if constexpr (sizeof(T) == 2) return launch_layout<T, 0, EPI>(a, b_kmajor, direct, s); break;
+      case 1: return launch_layout<T, 1, EPI>(a, b_kmajor, direct, s);
+      case 2: return launch_layout<T, 2, EPI>(a, b_kmajor, direct, s);
+      case 3: return launch_layout<T, 3, EPI>(a, b_kmajor, direct, s);
+      case 4: return launch_layout<T, 4, EPI>(a, b_kmajor, direct, s);
+      case 5: return launch_layout<T, 5, EPI>(a, b_kmajor, direct, s);
+      case 6: return launch_layout<T, 6, EPI>(a, b_kmajor, direct, s);
+      case 7: if constexpr (sizeof(T) == 2) return launch_layout<T, 7, EPI>(a, b_kmajor, direct, s); break;
+      default: break;
+    }
+    return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);
   }
 }
 
@@ -141,13 +189,26 @@ int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream)
   bool bv = aligned16(a.B, a.ldb, elt) && (a.sB1 * elt) % 16 == 0 && (a.sB2 * elt) % 16 == 0;
   if (epi == kEpiSwiglu) bv = bv && aligned16(a.B2, a.ldb, elt);
   a.b_vec = bv;
+  a.c_vec = aligned16(a.C, a.ldc, elt) && (a.sC1 * elt) % 16 == 0 && (a.sC2 * elt) % 16 == 0;
   if (a.gB <= 0) a.gB = 1;
   if (a.nb2 <= 0) a.nb2 = 1;
-  const TileChoice tc = choose_tile(dtype, a.N, a.K, epi);
-  switch (epi) {
-    case kEpiBias: return launch_epi<kEpiBias>(dtype, a, b_kmajor, tc, stream);
-    case kEpiSwiglu: return launch_epi<kEpiSwiglu>(dtype, a, b_kmajor, tc, stream);
-    default: return launch_epi<kEpiPlain>(dtype, a, b_kmajor, tc, stream);
+  // Direct global->LDS loads need whole 16-byte chunks: aligned operands, K-major B and K a
+  // multiple of the 128-byte step.
+  const bool direct = b_kmajor && a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) &&
+                      !(getenv("BIOPS_GEMM_NO_DIRECT"));
+  const int cfg = pick_cfg(dtype, a, epi);
+  switch (dtype) {
+    case BIOPS_F32:
+      return epi == kEpiSwiglu ? launch_typed<float, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                               : launch_typed<float, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+    case BIOPS_F16:
+      return epi == kEpiSwiglu ? launch_typed<f16_t, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                               : launch_typed<f16_t, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+    case BIOPS_BF16:
+      return epi == kEpiSwiglu ? launch_typed<bf16_t, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                               : launch_typed<bf16_t, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+    default:
+      return fail(BIOPS_ERR_DTYPE, "unsupported GEMM dtype %d", dtype);
   }
 }
 
@@ -164,11 +225,11 @@ __device__ __forceinline__ int64_t plan_find(const int64_t* plan, int64_t items,
 }
 
 template <typename T, int MODE>
-__global__ __launch_bounds__(kGemmThreads) void grouped_kernel(GroupedArgs a) {
+__global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
   constexpr int BM = kVarlenBM, BN = kVarlenBN;
   constexpr bool BKM = MODE == kGroupQK;  // K^T is K-major, V is N-major
-  using Tile = GemmTile<T, BM, BN, BKM>;
-  __shared__ __attribute__((aligned(16))) char smem[Tile::LDS_BYTES];
+  using Tile = GemmTile<T, BM, BN, 2, 2, 2, BKM, false>;
+  __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
   f32x16_t acc[Tile::FM][Tile::FN];
   constexpr int elt = sizeof(T);
   auto al = [](const void* p, int64_t off_elems) {
@@ -228,19 +289,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_kernel(GroupedArgs a) {
     const int64_t rows = M - m0, cols = N - n0;
 
     Tile::mainloop(smem, acc, A, lda, rows, avec, src, K);
-
-#pragma unroll
-    for (int i = 0; i < Tile::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < Tile::FN; ++j) {
-        const int c = Tile::acc_col(j);
-        if (c >= cols) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = Tile::acc_row(i, r);
-          if (row < rows) Num<T>::store(C + (int64_t)row * ldc + c, acc[i][j][r]);
-        }
-      }
+    const bool cvec = al(C, 0) && (ldc * elt) % 16 == 0;
+    Tile::template epilogue<false>(smem, acc, C, ldc, rows < BM ? (int)rows : BM,
+                                   cols < BN ? (int)cols : BN, nullptr, cvec);
   }
 }
 
@@ -252,9 +303,9 @@ static int launch_grouped_t(const GroupedArgs& a, int mode, hipStream_t s) {
   int64_t grid = (int64_t)cus * 2;
   if (a.total_tiles < grid) grid = a.total_tiles;
   if (mode == kGroupQK)
-    hipLaunchKernelGGL((grouped_kernel<T, kGroupQK>), dim3((unsigned)grid), dim3(kGemmThreads), 0, s, a);
+    hipLaunchKernelGGL((grouped_kernel<T, kGroupQK>), dim3((unsigned)grid), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((grouped_kernel<T, kGroupPV>), dim3((unsigned)grid), dim3(kGemmThreads), 0, s, a);
+    hipLaunchKernelGGL((grouped_kernel<T, kGroupPV>), dim3((unsigned)grid), dim3(256), 0, s, a);
   return check_launch("grouped_kernel");
 }
 
@@ -323,4 +374,12 @@ extern "C" int biops_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void
   a.lda = sAm; a.ldb = ldb; a.ldc = sCm;
   a.nb1 = 1; a.nb2 = 1; a.gB = 1;
   return launch_bmm(dtype, a, bias ? kEpiBias : kEpiPlain, kmajor, (hipStream_t)stream);
+}
+
+extern "C" int biops_gemm_tile_count(void) { return kNumCfg; }
+
+extern "C" int biops_set_gemm_tile(int cfg) {
+  if (cfg < -1 || cfg >= kNumCfg) return fail(BIOPS_ERR_ARG, "tile entry %d outside [-1, %d)", cfg, kNumCfg);
+  g_forced_cfg.store(cfg, std::memory_order_relaxed);
+  return BIOPS_OK;
 }

@@ -1,27 +1,29 @@
-// Fixed-schedule MFMA GEMM tile for gfx950 (CDNA4), shared by GEMM, BMM, grouped GEMM
+// Fixed-schedule MFMA GEMM tiles for gfx950 (CDNA4), shared by GEMM, BMM, grouped GEMM
 // (varlen attention) and the MoE expert GEMMs.
 //
 // Batch-invariance rule: every output element C[m,n] is produced by the same sequence of MFMA
-// instructions over the same K chunks, in the same order, whatever M, the batch size or the
-// tile the element falls in:
+// instructions over the same K chunks, in the same order, whatever M, the batch size, the block
+// tile or the load path:
 //   * K is consumed in fixed steps of 128 bytes (64 bf16/fp16 or 32 fp32 elements), in order;
-//   * inside a step, 16-byte chunks are paired (2q, 2q+1) and fed to one MFMA per pair
-//     (bf16/fp16: v_mfma_f32_32x32x16_{bf16,f16}); fp32 feeds the chunk pair element by element
-//     to four v_mfma_f32_32x32x2_f32;
-//   * out-of-range K is zero-filled in both operands, out-of-range rows/columns are zero-filled
-//     and never stored;
+//   * inside a step, 16-byte chunks are paired (2q, 2q+1), q = 0..3 in order, and each pair feeds
+//     one v_mfma_f32_32x32x16_{bf16,f16} (lane half 0 holds chunk 2q, half 1 chunk 2q+1);
+//     fp32 feeds the pair element by element to four v_mfma_f32_32x32x2_f32;
+//   * out-of-range K is zero in both operands; rows / columns outside the problem never reach
+//     the output;
 //   * there is no split-K: one workgroup owns the whole K loop of its tile.
-// The block tile (BM x BN) only decides which elements share a workgroup, not how any element
-// is computed, so it may be chosen from (dtype, N, K) without breaking invariance.
+// The block tile (BM x BN), the wavefront layout and the load path (direct-to-LDS or through
+// registers) only decide which elements share a workgroup and how operands reach LDS, never
+// the arithmetic of an element, so they may be chosen per problem shape.
 #pragma once
 
 #include "biops_common.h"
 
 namespace biops {
 
-constexpr int kGemmThreads = 256;  // 4 wavefronts in a 2 x 2 arrangement
-constexpr int kKBytes = 128;       // bytes of K per main-loop step
-constexpr int kLdsRow = 144;       // LDS row pitch: 128 B of K + 16 B pad (conflict-free b128 reads)
+constexpr int kKBytes = 128;  // bytes of K per main-loop step
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_cvoid_t;
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
@@ -62,7 +64,7 @@ template <typename T16> struct Bits16 {
 template <> struct Bits<bf16_t> : Bits16<bf16_t> {};
 template <> struct Bits<f16_t> : Bits16<f16_t> {};
 
-// Load one 16-byte chunk of `count_valid` (<= VEC) consecutive elements, zero beyond.
+// Load one 16-byte chunk of `valid` (<= VEC) consecutive elements, zero beyond.
 template <typename T>
 __device__ __forceinline__ u32x4_t load_chunk(const T* p, int valid, bool vec_ok) {
   constexpr int VEC = 16 / sizeof(T);
@@ -93,61 +95,82 @@ struct BSource {
   }
 };
 
-template <typename T, int BM, int BN, bool B_KMAJOR>
+// LDS tile layout: rows of 128 bytes (one K step), unpadded; 16-byte chunk c of row r lives in
+// slot c ^ ((r >> 1) & 7).  Sixteen consecutive rows reading the same chunk hit 16 distinct
+// (half-row, slot) bank groups, so the MFMA operand reads (ds_read_b128) are conflict-free.
+__device__ __forceinline__ int lds_off(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
+
+// Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN MFMA blocks).
+// STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
+// (A and K-major B, 16-byte aligned, K a multiple of the step); otherwise through registers.
+template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT>
 struct GemmTile {
+  static constexpr int THREADS = 64 * WGM * WGN;
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
-  static constexpr int WM = BM / 2, WN = BN / 2;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int FM = WM / 32, FN = WN / 32;
-  static constexpr int LDS_A = BM * kLdsRow, LDS_B = BN * kLdsRow;
+  static constexpr int LDS_A = BM * kKBytes, LDS_B = BN * kKBytes;
   static constexpr int LDS_STAGE = LDS_A + LDS_B;
-  static constexpr int LDS_BYTES = 2 * LDS_STAGE;
-  static constexpr int A_LOADS = BM / 32;  // 16-byte chunks per thread for the A tile
-  // B tile, K-major: BN rows of 8 chunks.  N-major: blocks of 4 K-rows x one 16-byte chunk.
-  static constexpr int B_LOADS_K = BN / 32;
-  static constexpr int B_BLOCKS_N = (BK / 4) * (BN / VEC) / kGemmThreads;
-  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
-  static_assert((BK / 4) * (BN / VEC) % kGemmThreads == 0, "N-major B tile split");
+  static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
+  // shared memory of a kernel using this tile: the LDS ring, or the staged output tile
+  static constexpr int EPI_BYTES = BM * BN * (int)sizeof(T);
+  static constexpr int SMEM_BYTES = LDS_BYTES > EPI_BYTES ? LDS_BYTES : EPI_BYTES;
+  // 16-byte chunk slots of one stage, and per-thread counts (last round may be partial)
+  static constexpr int A_SLOTS = BM * 8, B_SLOTS = BN * 8;
+  static constexpr int A_LOADS = (A_SLOTS + THREADS - 1) / THREADS;
+  static constexpr int B_LOADS = (B_SLOTS + THREADS - 1) / THREADS;
+  // N-major B (register path): blocks of 4 K-rows x one 16-byte chunk of columns
+  static constexpr int BN_BLOCKS = (BK / 4) * (BN / VEC);
+  static constexpr int BN_LOADS = (BN_BLOCKS + THREADS - 1) / THREADS;
+  static constexpr int B_REGS = B_KMAJOR ? B_LOADS : 4 * BN_LOADS;
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert(!DIRECT || B_KMAJOR, "direct loads need a K-major B");
+  static_assert(!DIRECT || (A_SLOTS % THREADS == 0 && B_SLOTS % THREADS == 0), "direct split");
+  static_assert(STAGES >= 2, "at least two stages");
+  static constexpr int LOADS_PER_STAGE = A_LOADS + B_LOADS;  // direct path, per thread
 
   struct Regs {
     u32x4_t a[A_LOADS];
-    u32x4_t b[B_KMAJOR ? B_LOADS_K : 4 * B_BLOCKS_N];
+    u32x4_t b[B_REGS];
   };
 
-  // A tile: rows [0, rows) valid (row r at A + r*lda), K columns [k0, K).
-  __device__ static __forceinline__ void load_a(Regs& R, const T* A, int64_t lda, int64_t rows,
-                                                int64_t k0, int64_t K, bool vec_ok) {
+  // ---------------------------------------------------------------- register path ----
+  __device__ static __forceinline__ void reg_load_a(Regs& R, const T* A, int64_t lda, int64_t rows,
+                                                    int64_t k0, int64_t K, bool vec_ok) {
     const int t = threadIdx.x;
     const int c = t & 7;
     const int64_t kk = k0 + c * VEC;
     const int valid = (int)(K - kk < VEC ? (K - kk < 0 ? 0 : K - kk) : VEC);
 #pragma unroll
     for (int p = 0; p < A_LOADS; ++p) {
-      const int r = (t >> 3) + 32 * p;
-      if (r < rows) R.a[p] = load_chunk<T>(A + (int64_t)r * lda + kk, valid, vec_ok);
+      const int s = t + THREADS * p;
+      const int r = s >> 3;
+      if (s < A_SLOTS && r < rows) R.a[p] = load_chunk<T>(A + (int64_t)r * lda + kk, valid, vec_ok);
       else R.a[p] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
 
-  __device__ static __forceinline__ void load_b(Regs& R, const BSource<T>& B, int64_t k0, int64_t K) {
+  __device__ static __forceinline__ void reg_load_b(Regs& R, const BSource<T>& B, int64_t k0, int64_t K) {
     const int t = threadIdx.x;
     if constexpr (B_KMAJOR) {
       const int c = t & 7;
       const int64_t kk = k0 + c * VEC;
       const int valid = (int)(K - kk < VEC ? (K - kk < 0 ? 0 : K - kk) : VEC);
 #pragma unroll
-      for (int p = 0; p < B_LOADS_K; ++p) {
-        const int r = (t >> 3) + 32 * p;
+      for (int p = 0; p < B_LOADS; ++p) {
+        const int s = t + THREADS * p;
+        const int r = s >> 3;
         int64_t local;
         const T* base = B.col_base(r, local);
-        if (local < B.ncols) R.b[p] = load_chunk<T>(base + local * B.ld + kk, valid, B.vec_ok);
+        if (s < B_SLOTS && local < B.ncols) R.b[p] = load_chunk<T>(base + local * B.ld + kk, valid, B.vec_ok);
         else R.b[p] = u32x4_t{0u, 0u, 0u, 0u};
       }
     } else {
       constexpr int CHUNKS = BN / VEC;
 #pragma unroll
-      for (int p = 0; p < B_BLOCKS_N; ++p) {
-        const int blk = t + kGemmThreads * p;
+      for (int p = 0; p < BN_LOADS; ++p) {
+        const int blk = t + THREADS * p;
         const int nc = blk % CHUNKS;
         const int kg = blk / CHUNKS;
         int64_t local;
@@ -157,49 +180,47 @@ struct GemmTile {
 #pragma unroll
         for (int kr = 0; kr < 4; ++kr) {
           const int64_t k = k0 + 4 * kg + kr;
-          if (k < K) R.b[4 * p + kr] = load_chunk<T>(base + k * B.ld + local, valid, B.vec_ok);
+          if (blk < BN_BLOCKS && k < K) R.b[4 * p + kr] = load_chunk<T>(base + k * B.ld + local, valid, B.vec_ok);
           else R.b[4 * p + kr] = u32x4_t{0u, 0u, 0u, 0u};
         }
       }
     }
   }
 
-  __device__ static __forceinline__ void store_lds(char* stage, const Regs& R) {
+  __device__ static __forceinline__ void reg_store(char* stage, const Regs& R) {
     const int t = threadIdx.x;
     char* As = stage;
     char* Bs = stage + LDS_A;
-    {
-      const int c = t & 7;
+    const int c = t & 7;
 #pragma unroll
-      for (int p = 0; p < A_LOADS; ++p) {
-        const int r = (t >> 3) + 32 * p;
-        *reinterpret_cast<u32x4_t*>(As + r * kLdsRow + c * 16) = R.a[p];
-      }
+    for (int p = 0; p < A_LOADS; ++p) {
+      const int s = t + THREADS * p;
+      if (s < A_SLOTS) *reinterpret_cast<u32x4_t*>(As + lds_off(s >> 3, c)) = R.a[p];
     }
     if constexpr (B_KMAJOR) {
-      const int c = t & 7;
 #pragma unroll
-      for (int p = 0; p < B_LOADS_K; ++p) {
-        const int r = (t >> 3) + 32 * p;
-        *reinterpret_cast<u32x4_t*>(Bs + r * kLdsRow + c * 16) = R.b[p];
+      for (int p = 0; p < B_LOADS; ++p) {
+        const int s = t + THREADS * p;
+        if (s < B_SLOTS) *reinterpret_cast<u32x4_t*>(Bs + lds_off(s >> 3, c)) = R.b[p];
       }
     } else {
       constexpr int CHUNKS = BN / VEC;
 #pragma unroll
-      for (int p = 0; p < B_BLOCKS_N; ++p) {
-        const int blk = t + kGemmThreads * p;
+      for (int p = 0; p < BN_LOADS; ++p) {
+        const int blk = t + THREADS * p;
+        if (blk >= BN_BLOCKS) continue;
         const int nc = blk % CHUNKS;
-        const int kg = blk / CHUNKS;
+        const int kg = blk / CHUNKS;  // K rows 4kg .. 4kg+3 of the step
         const u32x4_t* in = &R.b[4 * p];
         if constexpr (sizeof(T) == 4) {
-          // 4 K-rows x 4 columns of fp32: column j gets {in[0][j], .., in[3][j]}.
+          // 4 K-rows x 4 columns of fp32: column j gets {in[0][j], .., in[3][j]} = chunk kg.
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             u32x4_t o = {in[0][j], in[1][j], in[2][j], in[3][j]};
-            *reinterpret_cast<u32x4_t*>(Bs + (nc * 4 + j) * kLdsRow + kg * 16) = o;
+            *reinterpret_cast<u32x4_t*>(Bs + lds_off(nc * 4 + j, kg)) = o;
           }
         } else {
-          // 4 K-rows x 8 columns of 16-bit values: column j gets 4 halves (8 bytes).
+          // 4 K-rows x 8 columns of 16-bit values: column j gets 4 halves = half of chunk kg/2.
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int d = j >> 1;
@@ -212,38 +233,94 @@ struct GemmTile {
               hi = (in[2][d] & 0x0000ffffu) | (in[3][d] << 16);
             }
             u32x2_t o = {lo, hi};
-            *reinterpret_cast<u32x2_t*>(Bs + (nc * 8 + j) * kLdsRow + kg * 8) = o;
+            *reinterpret_cast<u32x2_t*>(Bs + lds_off(nc * 8 + j, kg >> 1) + (kg & 1) * 8) = o;
           }
         }
       }
     }
   }
 
-  __device__ static __forceinline__ void compute(const char* stage, f32x16_t (&acc)[FM][FN]) {
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int wm = w >> 1, wn = w & 1;
-    const int lr = lane & 31, lb = lane >> 5;
-    const char* As = stage + (wm * WM + lr) * kLdsRow + lb * 16;
-    const char* Bs = stage + LDS_A + (wn * WN + lr) * kLdsRow + lb * 16;
+  // ------------------------------------------------------------------ direct path ----
+  // Slot s of the stage (s = THREADS*p + thread) is written by lane s%64 of instruction p at
+  // LDS byte 16*s (row s/8, slot s%8); that slot holds logical chunk (s%8) ^ ((row>>1)&7), so
+  // the lane fetches exactly that chunk.  Rows past the problem are clamped to its last row
+  // (their products are never stored).
+  __device__ static __forceinline__ void direct_load(char* stage, const T* A, int64_t lda, int64_t rows,
+                                                     const BSource<T>& B, int64_t k0) {
+    const int t = threadIdx.x;
+    const int wbase = t & ~63;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      u32x4_t a[FM], b[FN];
+    for (int p = 0; p < A_SLOTS / THREADS; ++p) {
+      const int s = t + THREADS * p;
+      const int r = s >> 3;
+      const int c = (s & 7) ^ ((r >> 1) & 7);
+      const int64_t rr = r < rows ? r : rows - 1;
+      const T* src = A + rr * lda + k0 + c * VEC;
+      __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
+                                       (lds_void_t*)(stage + (THREADS * p + wbase) * 16), 16, 0, 0);
+    }
+    char* Bs = stage + LDS_A;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-        a[i] = *reinterpret_cast<const u32x4_t*>(As + i * 32 * kLdsRow + q * 32);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        b[j] = *reinterpret_cast<const u32x4_t*>(Bs + j * 32 * kLdsRow + q * 32);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], a[i], b[j]);
+    for (int p = 0; p < B_SLOTS / THREADS; ++p) {
+      const int s = t + THREADS * p;
+      const int r = s >> 3;
+      const int c = (s & 7) ^ ((r >> 1) & 7);
+      int64_t local;
+      const T* base = B.col_base(r, local);
+      if (local >= B.ncols) local = B.ncols - 1;
+      const T* src = base + local * B.ld + k0 + c * VEC;
+      __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
+                                       (lds_void_t*)(Bs + (THREADS * p + wbase) * 16), 16, 0, 0);
     }
   }
 
-  // Full K loop of one tile into acc (zeroed here).  The caller guarantees that the LDS is not
-  // being read by another wavefront on entry (a barrier separates consecutive tiles).
+  // ---------------------------------------------------------------------- compute ----
+  __device__ static __forceinline__ void load_frags(const char* stage, int q, u32x4_t (&a)[FM], u32x4_t (&b)[FN]) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int wm = w / WGN, wn = w % WGN;
+    const int lr = lane & 31, lb = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      a[i] = *reinterpret_cast<const u32x4_t*>(stage + lds_off(wm * WM + i * 32 + lr, 2 * q + lb));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
+  }
+
+  // One K step: the operand fragments of step q+1 are read from LDS while the MFMAs of step q
+  // run (two fragment buffers); the MFMA order per accumulator is q = 0, 1, 2, 3.
+  __device__ static __forceinline__ void compute(const char* stage, f32x16_t (&acc)[FM][FN]) {
+    u32x4_t a[2][FM], b[2][FN];
+    load_frags(stage, 0, a[0], b[0]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q < 3) load_frags(stage, q + 1, a[(q + 1) & 1], b[(q + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], a[q & 1][i], b[q & 1][j]);
+    }
+  }
+
+  // Workgroup barrier that orders this thread's LDS reads/writes only: in-flight global loads
+  // (the prefetch of later stages) keep running across it, which a fenced __syncthreads()
+  // would drain.  Completion of the direct-to-LDS loads is tracked separately (wait_loads).
+  // The "memory" clobber keeps the compiler from moving memory accesses across it.
+  __device__ static __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  // Waits until at most `n` direct loads of this thread are still in flight.
+  template <int N>
+  __device__ static __forceinline__ void wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // s_waitcnt: vmcnt[3:0] | expcnt[6:4]=7 | lgkmcnt[11:8]=15 | vmcnt[5:4] at [15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  }
+
+  // Full K loop of one tile into acc (zeroed here).  The caller guarantees that no wavefront
+  // reads the LDS ring on entry (a barrier separates consecutive tiles).
   __device__ static __forceinline__ void mainloop(char* smem, f32x16_t (&acc)[FM][FN],
                                                   const T* A, int64_t lda, int64_t rows, bool a_vec,
                                                   const BSource<T>& B, int64_t K) {
@@ -255,33 +332,109 @@ struct GemmTile {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     const int64_t KT = cdiv(K, BK);
     if (KT == 0) return;
-    Regs R;
-    load_a(R, A, lda, rows, 0, K, a_vec);
-    load_b(R, B, 0, K);
-    store_lds(smem, R);
-    __syncthreads();
-    for (int64_t kt = 0; kt < KT; ++kt) {
-      const int cur = (int)(kt & 1);
-      const bool more = kt + 1 < KT;
-      if (more) {
-        load_a(R, A, lda, rows, (kt + 1) * BK, K, a_vec);
-        load_b(R, B, (kt + 1) * BK, K);
+    if constexpr (DIRECT) {
+      (void)a_vec;
+      constexpr int AHEAD = STAGES - 1;  // tiles in flight beyond the one being computed
+#pragma unroll
+      for (int s = 0; s < AHEAD; ++s)
+        if (s < KT) direct_load(smem + s * LDS_STAGE, A, lda, rows, B, (int64_t)s * BK);
+      int cur = 0;            // stage of tile kt
+      int nxt = AHEAD;        // stage of tile kt + AHEAD (== stage of tile kt - 1)
+      for (int64_t kt = 0; kt < KT; ++kt) {
+        // tile kt landed once at most min(AHEAD-1, KT-1-kt) later tiles remain in flight
+        if (KT - 1 - kt >= AHEAD - 1) wait_loads<(AHEAD - 1) * LOADS_PER_STAGE>();
+        else wait_loads<0>();
+        lds_barrier();  // tile kt visible to all; every wave is done with tile kt - 1
+        if (kt + AHEAD < KT)
+          direct_load(smem + nxt * LDS_STAGE, A, lda, rows, B, (kt + AHEAD) * BK);
+        compute(smem + cur * LDS_STAGE, acc);
+        cur = cur + 1 == STAGES ? 0 : cur + 1;
+        nxt = nxt + 1 == STAGES ? 0 : nxt + 1;
       }
-      compute(smem + cur * LDS_STAGE, acc);
-      if (more) store_lds(smem + (cur ^ 1) * LDS_STAGE, R);
-      __syncthreads();
+      lds_barrier();
+    } else {
+      Regs R;
+      reg_load_a(R, A, lda, rows, 0, K, a_vec);
+      reg_load_b(R, B, 0, K);
+      reg_store(smem, R);
+      lds_barrier();
+      for (int64_t kt = 0; kt < KT; ++kt) {
+        const int cur = (int)(kt & 1);
+        const bool more = kt + 1 < KT;
+        if (more) {
+          reg_load_a(R, A, lda, rows, (kt + 1) * BK, K, a_vec);
+          reg_load_b(R, B, (kt + 1) * BK, K);
+        }
+        compute(smem + cur * LDS_STAGE, acc);
+        if (more) reg_store(smem + (cur ^ 1) * LDS_STAGE, R);
+        lds_barrier();
+      }
     }
+  }
+
+  // Epilogue.  The rounded tile is staged in LDS (row-major, 16-byte chunk k of row r stored
+  // at chunk position k ^ (r & 7) -- masked to the chunks of a row -- so the two
+  // half-wavefronts, 4 rows apart, write disjoint banks) and written to C with 16-byte stores.  SWIGLU: gate / up accumulators of one output sit in
+  // blocks (i, j) / (i, j+1) of the same lane; the stored value is
+  // round(round(silu(round(g))) * round(u)) and the tile is BN/2 wide.  Otherwise the value is
+  // round(acc + bias[col]) (bias may be null: no add).  Ends with a barrier, so the LDS ring
+  // is free for the next tile.
+  template <bool SWIGLU>
+  __device__ static __forceinline__ void epilogue(char* smem, f32x16_t (&acc)[FM][FN], T* C,
+                                                  int64_t ldc, int rows, int cols, const T* bias,
+                                                  bool c_vec) {
+    constexpr int OUTW = SWIGLU ? BN / 2 : BN;
+    constexpr int PITCH = OUTW * (int)sizeof(T);
+    constexpr int SWZ = OUTW / VEC >= 8 ? 7 : OUTW / VEC - 1;  // chunk swizzle stays inside the row
+    static_assert(BM * PITCH <= SMEM_BYTES, "epilogue tile must fit the shared memory");
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; j += (SWIGLU ? 2 : 1)) {
+        const int c = acc_col(j);
+        const int col = SWIGLU ? ((c >> 6) << 5) + (c & 31) : c;
+        const float bv = (!SWIGLU && bias && col < cols) ? Num<T>::load(bias + col) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v;
+          if constexpr (SWIGLU) {
+            const float g = Num<T>::round(acc[i][j][r]);
+            const float u = Num<T>::round(acc[i][j + 1][r]);
+            v = Num<T>::round(g / (1.0f + expf(-g))) * u;
+          } else {
+            v = bias ? acc[i][j][r] + bv : acc[i][j][r];
+          }
+          const int row = acc_row(i, r);
+          const int pos = (((col / VEC) ^ (row & SWZ)) * VEC) + (col % VEC);
+          Num<T>::store(reinterpret_cast<T*>(smem + row * PITCH) + pos, v);
+        }
+      }
+    lds_barrier();
+    constexpr int CH = OUTW / VEC;
+    for (int id = threadIdx.x; id < BM * CH; id += THREADS) {
+      const int r = id / CH;
+      const int c0 = (id - r * CH) * VEC;
+      if (r >= rows || c0 >= cols) continue;
+      const char* src = smem + r * PITCH + (((c0 / VEC) ^ (r & SWZ)) * 16);
+      T* dst = C + (int64_t)r * ldc + c0;
+      if (c_vec && c0 + VEC <= cols) {
+        *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
+      } else {
+        for (int e = 0; e < VEC && c0 + e < cols; ++e) dst[e] = reinterpret_cast<const T*>(src)[e];
+      }
+    }
+    lds_barrier();
   }
 
   // Tile-local coordinates of accumulator register r of block (i, j) for this lane.
   __device__ static __forceinline__ int acc_row(int i, int r) {
     const int lane = threadIdx.x & 63;
-    const int wm = (threadIdx.x >> 6) >> 1;
+    const int wm = (threadIdx.x >> 6) / WGN;
     return wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
   }
   __device__ static __forceinline__ int acc_col(int j) {
     const int lane = threadIdx.x & 63;
-    const int wn = (threadIdx.x >> 6) & 1;
+    const int wn = (threadIdx.x >> 6) % WGN;
     return wn * WN + j * 32 + (lane & 31);
   }
 };

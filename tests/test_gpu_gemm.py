@@ -169,3 +169,35 @@ def test_bmm_empty():
     a = gpu(randn(0, 3, 4, seed=1))
     b = gpu(randn(0, 4, 5, seed=2))
     assert bmm_persistent(a, b).shape == (0, 3, 5)
+
+
+@pytest.fixture
+def tile_menu():
+    from batch_invariant_ops import _native as nat
+
+    lib = nat.load()
+    yield lib
+    lib.biops_set_gemm_tile(-1)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("m", "k", "n", "layout"), (
+    (300, 2048, 520, "w"),      # K-major B (nn.Linear), direct-to-LDS loads
+    (129, 200, 136, "w"),       # K not a multiple of the step: register path
+    (77, 1024, 256, "rowmajor"),  # N-major B
+    (33, 65, 47, "w"),          # unaligned rows
+))
+def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout):
+    """All entries of the tile menu compute each element with the same MFMA sequence."""
+    x = gpu(randn(m, k, seed=5000 + m, dtype=dtype))
+    if layout == "w":
+        b = gpu(randn(n, k, seed=5001 + n, dtype=dtype)).t()
+    else:
+        b = gpu(randn(k, n, seed=5001 + n, dtype=dtype))
+    bias = gpu(randn(n, seed=5002, dtype=dtype))
+    tile_menu.biops_set_gemm_tile(-1)
+    ref = matmul_persistent(x, b, bias)
+    for cfg in range(tile_menu.biops_gemm_tile_count()):
+        assert tile_menu.biops_set_gemm_tile(cfg) == 0
+        assert_bitwise(matmul_persistent(x, b, bias), ref, f"tile entry {cfg}")
+        assert_bitwise(matmul_persistent(x[5:6], b, bias), ref[5:6], f"tile entry {cfg}, one row")
