@@ -103,8 +103,8 @@ int biops_gemm_tile_count(void);
 
 /* Force GEMM tile entry `cfg` for every later GEMM/BMM launch in the process (-1 restores the
  * automatic choice, which is the default; the BIOPS_GEMM_CFG environment variable sets the
- * initial value).  Entries 0 and 7 have no fp32 kernel and fall back to the automatic choice
- * for fp32.  For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
+ * initial value).  Entries 0, 7 and 9 have no fp32 kernel and fall back to the automatic
+ * choice for fp32.  For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
 int biops_set_gemm_tile(int cfg);
 
 /* --------------------------------------------------------------- row reductions ---- */

@@ -11,23 +11,29 @@ namespace biops {
 // Every entry computes each output element with the same MFMA sequence (see gemm_core.h); the
 // entries differ in block tile, wavefront layout and LDS ring depth only.
 template <int ID> struct Cfg;
-#define BIOPS_CFG(ID, BM_, BN_, WGM_, WGN_, ST_, PERCU_)                             \
+#define BIOPS_CFG(ID, BM_, BN_, WGM_, WGN_, ST_, PERCU_, PP_)                        \
   template <> struct Cfg<ID> {                                                    \
     static constexpr int bm = BM_, bn = BN_, wgm = WGM_, wgn = WGN_, stages = ST_;   \
     static constexpr int threads = 64 * WGM_ * WGN_, per_cu = PERCU_;             \
     static constexpr int waves_per_eu = (WGM_ * WGN_ * PERCU_ + 3) / 4;           \
+    static constexpr bool pingpong = PP_;                                         \
+    static constexpr bool persist = BM_ * BN_ < 256 * 256;                       \
   };
-//         id   BM   BN  WGM WGN stages  workgroups/CU
-BIOPS_CFG(0, 256, 256, 2, 2, 2, 1)
-BIOPS_CFG(1, 256, 128, 2, 2, 3, 1)
-BIOPS_CFG(2, 128, 128, 2, 2, 2, 2)
-BIOPS_CFG(3, 128, 64, 2, 2, 4, 1)
-BIOPS_CFG(4, 64, 64, 2, 2, 4, 2)
-BIOPS_CFG(5, 32, 64, 1, 2, 8, 1)
-BIOPS_CFG(6, 32, 32, 1, 1, 8, 1)
-BIOPS_CFG(7, 256, 256, 2, 4, 2, 1)
+//         id   BM   BN  WGM WGN stages  workgroups/CU  ping-pong
+BIOPS_CFG(0, 256, 256, 2, 4, 2, 1, true)
+BIOPS_CFG(1, 256, 128, 2, 2, 3, 1, false)
+BIOPS_CFG(2, 128, 128, 2, 2, 2, 2, false)
+BIOPS_CFG(3, 128, 64, 2, 2, 4, 1, false)
+BIOPS_CFG(4, 64, 64, 2, 2, 4, 2, false)
+BIOPS_CFG(5, 32, 64, 1, 2, 4, 2, false)
+BIOPS_CFG(6, 32, 32, 1, 1, 4, 4, false)
+BIOPS_CFG(7, 256, 256, 2, 4, 2, 1, false)
+BIOPS_CFG(8, 128, 128, 2, 2, 4, 1, false)
+BIOPS_CFG(9, 128, 256, 2, 2, 3, 1, false)
+BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false)
+BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false)
 #undef BIOPS_CFG
-constexpr int kNumCfg = 8;
+constexpr int kNumCfg = 12;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
 // Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
@@ -35,67 +41,80 @@ constexpr int kNumCfg = 8;
 // applied to rounded bmm outputs -- where gate and up accumulators of one output sit in
 // adjacent 32-column MFMA blocks of the same wavefront.
 template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
+__device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* smem) {
+  using C = Cfg<CFG>;
+  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
+  constexpr int BM = C::bm, BN = C::bn;
+  constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
+  typename Tile::Acc acc[Tile::FM][Tile::FN];
+
+  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
+  const uint32_t tpb = tiles_m * tiles_n;
+  const uint32_t nb2 = (uint32_t)args.nb2, gB = (uint32_t)args.gB;
+  const uint32_t b = t / tpb;
+  const uint32_t in_b = t - b * tpb;
+  // grouped order: 8 tile-rows form a group walked column by column
+  const uint32_t per_group = 8u * tiles_n;
+  const uint32_t group = in_b / per_group;
+  const uint32_t first = group * 8u;
+  const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
+  const uint32_t in_group = in_b - group * per_group;
+  const uint32_t tn = in_group / gsize;
+  const uint32_t tm = first + (in_group - tn * gsize);
+  const uint32_t b1 = b / nb2;
+  const uint32_t b2 = b - b1 * nb2;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * kCols;
+
+  const T* A = reinterpret_cast<const T*>(args.A) + b1 * args.sA1 + b2 * args.sA2 + m0 * args.lda;
+  const int64_t boff = b1 * args.sB1 + (b2 / gB) * args.sB2 + (BKM ? n0 * args.ldb : n0);
+  BSource<T> src;
+  src.p0 = reinterpret_cast<const T*>(args.B) + boff;
+  src.p1 = EPI == kEpiSwiglu ? reinterpret_cast<const T*>(args.B2) + boff : src.p0;
+  src.ld = args.ldb;
+  src.ncols = args.N - n0;
+  src.swiglu = EPI == kEpiSwiglu;
+  src.vec_ok = args.b_vec != 0;
+  const int64_t rows = args.M - m0;
+  const int64_t cols = args.N - n0;
+
+  if constexpr (C::pingpong && DIRECT) Tile::mainloop_pingpong(smem, acc, A, args.lda, rows, src, args.K);
+  else Tile::mainloop(smem, acc, A, args.lda, rows, args.a_vec != 0, src, args.K);
+
+  T* Cp = reinterpret_cast<T*>(args.C) + b1 * args.sC1 + b2 * args.sC2 + m0 * args.ldc + n0;
+  const T* bias = (EPI != kEpiSwiglu && args.bias) ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
+  Tile::template epilogue<EPI == kEpiSwiglu>(smem, acc, Cp, args.ldc, rows < BM ? (int)rows : BM,
+                                             cols < kCols ? (int)cols : kCols, bias, args.c_vec != 0);
+}
+
+// Persistent entries walk tiles t = slot, slot + G, ... (slot = XCD-aware rank of the
+// workgroup); the large-tile entries run one tile per workgroup (grid = tiles, same XCD-aware
+// order), which keeps their register budget for the accumulators.
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
 __global__ __launch_bounds__(Cfg<CFG>::threads)
 __attribute__((amdgpu_waves_per_eu(Cfg<CFG>::waves_per_eu, Cfg<CFG>::waves_per_eu)))
 void bmm_kernel(BmmArgs args) {
   using C = Cfg<CFG>;
   using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
-  constexpr int BM = C::bm, BN = C::bn;
-  constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
   __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
-  f32x16_t acc[Tile::FM][Tile::FN];
-
-  // Tile indices stay 32-bit (the launcher guarantees fewer than 2^31 tiles).
   const uint32_t G = gridDim.x;
   const uint32_t total = (uint32_t)args.total;
-  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
-  const uint32_t tpb = tiles_m * tiles_n;
-  const uint32_t nb2 = (uint32_t)args.nb2, gB = (uint32_t)args.gB;
-  for (uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G); t < total; t += G) {
-    const uint32_t b = t / tpb;
-    const uint32_t in_b = t - b * tpb;
-    // grouped order: 8 tile-rows form a group walked column by column
-    const uint32_t per_group = 8u * tiles_n;
-    const uint32_t group = in_b / per_group;
-    const uint32_t first = group * 8u;
-    const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
-    const uint32_t in_group = in_b - group * per_group;
-    const uint32_t tn = in_group / gsize;
-    const uint32_t tm = first + (in_group - tn * gsize);
-    const uint32_t b1 = b / nb2;
-    const uint32_t b2 = b - b1 * nb2;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * kCols;
-
-    const T* A = reinterpret_cast<const T*>(args.A) + b1 * args.sA1 + b2 * args.sA2 + m0 * args.lda;
-    const int64_t boff = b1 * args.sB1 + (b2 / gB) * args.sB2 + (BKM ? n0 * args.ldb : n0);
-    BSource<T> src;
-    src.p0 = reinterpret_cast<const T*>(args.B) + boff;
-    src.p1 = EPI == kEpiSwiglu ? reinterpret_cast<const T*>(args.B2) + boff : src.p0;
-    src.ld = args.ldb;
-    src.ncols = args.N - n0;
-    src.swiglu = EPI == kEpiSwiglu;
-    src.vec_ok = args.b_vec != 0;
-    const int64_t rows = args.M - m0;
-    const int64_t cols = args.N - n0;
-
-    Tile::mainloop(smem, acc, A, args.lda, rows, args.a_vec != 0, src, args.K);
-
-    T* Cp = reinterpret_cast<T*>(args.C) + b1 * args.sC1 + b2 * args.sC2 + m0 * args.ldc + n0;
-    const T* bias = (EPI != kEpiSwiglu && args.bias) ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
-    Tile::template epilogue<EPI == kEpiSwiglu>(smem, acc, Cp, args.ldc, rows < BM ? (int)rows : BM,
-                                               cols < kCols ? (int)cols : kCols, bias, args.c_vec != 0);
+  if constexpr (C::persist) {
+    for (uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G); t < total; t += G)
+      bmm_tile<T, CFG, BKM, DIRECT, EPI>(args, t, smem);
+  } else {
+    const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G);
+    if (t < total) bmm_tile<T, CFG, BKM, DIRECT, EPI>(args, t, smem);
   }
 }
 
 // -------------------------------------------------------------- tile selection ----
-// Measured full-chip throughput of each entry on large bf16 problems (TFLOP/s, MI355X), used
-// to estimate which entry finishes a problem first: a problem of T tiles on S = CUs x
-// (workgroups per CU) slots takes ceil(T / S) rounds of one tile time, and one tile time is
-// proportional to BM x BN x (workgroups per CU) / throughput.
-static const double kCfgRate[kNumCfg] = {520, 700, 830, 475, 500, 185, 108, 900};
-static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 256};
-static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 256};
-static const int kCfgPerCu[kNumCfg] = {1, 1, 2, 1, 2, 1, 1, 1};
+// Measured full-chip throughput of each entry on large bf16 problems (TFLOP/s, MI355X).  A
+// compute unit works through ceil(tiles / CUs) tiles, each costing BM x BN / throughput (two
+// resident workgroups share the unit, so they do not finish sooner), and the entry with the
+// smallest estimate is launched.
+static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 910, 570, 670, 900, 900};
+static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 256, 128, 128, 256, 128};
+static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 256, 128, 256, 128, 256};
 
 // Forced tile entry (-1: automatic).  Initialised from BIOPS_GEMM_CFG, settable through
 // biops_set_gemm_tile; every entry yields the same bits, so forcing one only changes speed.
@@ -116,18 +135,16 @@ static int forced_cfg() {
 static int pick_cfg(int dtype, const BmmArgs& a, int epi) {
   if (epi == kEpiSwiglu) return 2;
   const int forced = forced_cfg();
-  if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7)))
+  if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7 || forced == 9)))
     return forced;
   const int cus = device_cus();
   const int64_t batch = a.nb1 * a.nb2;
   int best = 2;
   double best_cost = 1e300;
   for (int c = 0; c < kNumCfg; ++c) {
-    if (dtype == BIOPS_F32 && (c == 0 || c == 7)) continue;  // fp32 accumulators need the smaller tiles
+    if (dtype == BIOPS_F32 && (c == 0 || c == 7 || c == 9)) continue;  // no fp32 kernel
     const int64_t tiles = batch * cdiv(a.M, kCfgBM[c]) * cdiv(a.N, kCfgBN[c]);
-    const int64_t slots = (int64_t)cus * kCfgPerCu[c];
-    const double rounds = (double)cdiv(tiles, slots);
-    const double cost = rounds * (double)kCfgBM[c] * kCfgBN[c] * kCfgPerCu[c] / kCfgRate[c];
+    const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / kCfgRate[c];
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
   return best;
@@ -145,7 +162,7 @@ static int launch_cfg(const BmmArgs& a0, hipStream_t stream) {
   if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int cus = device_cus();
   if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
-  int64_t grid = (int64_t)cus * C::per_cu;
+  int64_t grid = C::persist ? (int64_t)cus * C::per_cu : a.total;
   if (a.total < grid) grid = a.total;
   hipLaunchKernelGGL((bmm_kernel<T, CFG, BKM, DIRECT, EPI>), dim3((unsigned)grid), dim3(C::threads),
                      0, stream, a);
@@ -173,6 +190,10 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 5: return launch_layout<T, 5, EPI>(a, b_kmajor, direct, s);
       case 6: return launch_layout<T, 6, EPI>(a, b_kmajor, direct, s);
       case 7: if constexpr (sizeof(T) == 2) return launch_layout<T, 7, EPI>(a, b_kmajor, direct, s); break;
+      case 8: return launch_layout<T, 8, EPI>(a, b_kmajor, direct, s);
+      case 9: if constexpr (sizeof(T) == 2) return launch_layout<T, 9, EPI>(a, b_kmajor, direct, s); break;
+      case 10: return launch_layout<T, 10, EPI>(a, b_kmajor, direct, s);
+      case 11: return launch_layout<T, 11, EPI>(a, b_kmajor, direct, s);
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);
@@ -230,7 +251,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
   constexpr bool BKM = MODE == kGroupQK;  // K^T is K-major, V is N-major
   using Tile = GemmTile<T, BM, BN, 2, 2, 2, BKM, false>;
   __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
-  f32x16_t acc[Tile::FM][Tile::FN];
+  typename Tile::Acc acc[Tile::FM][Tile::FN];
   constexpr int elt = sizeof(T);
   auto al = [](const void* p, int64_t off_elems) {
     return ((reinterpret_cast<uintptr_t>(p) + (uintptr_t)off_elems * elt) % 16) == 0;

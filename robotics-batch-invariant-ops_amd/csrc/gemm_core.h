@@ -7,7 +7,7 @@
 //   * K is consumed in fixed steps of 128 bytes (64 bf16/fp16 or 32 fp32 elements), in order;
 //   * inside a step, 16-byte chunks are paired (2q, 2q+1), q = 0..3 in order, and each pair feeds
 //     one v_mfma_f32_32x32x16_{bf16,f16} (lane half 0 holds chunk 2q, half 1 chunk 2q+1);
-//     fp32 feeds the pair element by element to four v_mfma_f32_32x32x2_f32;
+//     fp32 feeds the pair element by element (s = 0..3) to four v_mfma_f32_32x32x2_f32;
 //   * out-of-range K is zero in both operands; rows / columns outside the problem never reach
 //     the output;
 //   * there is no split-K: one workgroup owns the whole K loop of its tile.
@@ -25,6 +25,7 @@ constexpr int kKBytes = 128;  // bytes of K per main-loop step
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void global_cvoid_t;
 
+// One 32x32 output block, one chunk pair of the step (32 x 32 fp32 accumulators: 16 per lane).
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
   __device__ static __forceinline__ void step(f32x16_t& acc, const u32x4_t& a, const u32x4_t& b) {
@@ -79,7 +80,7 @@ __device__ __forceinline__ u32x4_t load_chunk(const T* p, int valid, bool vec_ok
 // Where the B operand of one tile comes from.  Logical tile column c (0..BN-1) maps to
 // problem column n0 + c, or, in SwiGLU mode, to column n0/2 + (c/64)*32 + c%32 of the gate
 // matrix (c/32 even) or the up matrix (c/32 odd), so that one wavefront holds gate and up
-// accumulators of the same output element.
+// accumulators of the same output element in adjacent 32x32 blocks.
 template <typename T>
 struct BSource {
   const T* p0;      // gate / plain B
@@ -100,7 +101,7 @@ struct BSource {
 // (half-row, slot) bank groups, so the MFMA operand reads (ds_read_b128) are conflict-free.
 __device__ __forceinline__ int lds_off(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
 
-// Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN MFMA blocks).
+// Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN 32x32 blocks).
 // STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
 // (A and K-major B, 16-byte aligned, K a multiple of the step); otherwise through registers.
 template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT>
@@ -110,6 +111,7 @@ struct GemmTile {
   static constexpr int BK = kKBytes / (int)sizeof(T);
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int FM = WM / 32, FN = WN / 32;
+  typedef f32x16_t Acc;
   static constexpr int LDS_A = BM * kKBytes, LDS_B = BN * kKBytes;
   static constexpr int LDS_STAGE = LDS_A + LDS_B;
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
@@ -288,18 +290,43 @@ struct GemmTile {
       b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
   }
 
-  // One K step: the operand fragments of step q+1 are read from LDS while the MFMAs of step q
-  // run (two fragment buffers); the MFMA order per accumulator is q = 0, 1, 2, 3.
-  __device__ static __forceinline__ void compute(const char* stage, f32x16_t (&acc)[FM][FN]) {
-    u32x4_t a[2][FM], b[2][FN];
-    load_frags(stage, 0, a[0], b[0]);
+  // K group g (0, 1) of a step = MFMA steps q = 2g, 2g+1 (64 bytes of K).
+  struct Frags {
+    u32x4_t a[2][FM];
+    u32x4_t b[2][FN];
+  };
+  __device__ static __forceinline__ void load_group(const char* stage, int g, Frags& f) {
+    load_frags(stage, 2 * g, f.a[0], f.b[0]);
+    load_frags(stage, 2 * g + 1, f.a[1], f.b[1]);
+  }
+  __device__ static __forceinline__ void mfma_group(Acc (&acc)[FM][FN], const Frags& f) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q < 3) load_frags(stage, q + 1, a[(q + 1) & 1], b[(q + 1) & 1]);
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], a[q & 1][i], b[q & 1][j]);
+        for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], f.a[h][i], f.b[h][j]);
+  }
+
+  // One K step (groups 0 then 1).  Small wave tiles read both groups' fragments before the
+  // MFMAs (two buffers); large ones read one group at a time to save registers.
+  static constexpr bool FRAG_DB = FM + FN <= 4;
+  __device__ static __forceinline__ void compute(const char* stage, Acc (&acc)[FM][FN]) {
+    if constexpr (FRAG_DB) {
+      Frags f0, f1;
+      load_group(stage, 0, f0);
+      load_group(stage, 1, f1);
+      mfma_group(acc, f0);
+      mfma_group(acc, f1);
+    } else {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        Frags f;
+        load_group(stage, g, f);
+        mfma_group(acc, f);
+        // keep the next group's fragment reads behind these MFMAs (one live fragment set)
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
@@ -310,6 +337,9 @@ struct GemmTile {
   __device__ static __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
+  // Barrier that also lets this thread's own LDS reads stay in flight (for reads of a stage
+  // that nobody overwrites before the next barrier).
+  __device__ static __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
   // Waits until at most `n` direct loads of this thread are still in flight.
   template <int N>
@@ -321,7 +351,7 @@ struct GemmTile {
 
   // Full K loop of one tile into acc (zeroed here).  The caller guarantees that no wavefront
   // reads the LDS ring on entry (a barrier separates consecutive tiles).
-  __device__ static __forceinline__ void mainloop(char* smem, f32x16_t (&acc)[FM][FN],
+  __device__ static __forceinline__ void mainloop(char* smem, Acc (&acc)[FM][FN],
                                                   const T* A, int64_t lda, int64_t rows, bool a_vec,
                                                   const BSource<T>& B, int64_t K) {
 #pragma unroll
@@ -332,7 +362,43 @@ struct GemmTile {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     const int64_t KT = cdiv(K, BK);
     if (KT == 0) return;
-    if constexpr (DIRECT) {
+    if constexpr (DIRECT && STAGES >= 3) {
+      // Software-pipelined schedule: the fragments of K group 1 of tile kt and of group 0 of
+      // tile kt+1 are read from LDS while the MFMAs of the previous group run; the barrier
+      // that publishes tile kt+1 sits between the two MFMA groups of tile kt.
+      (void)a_vec;
+      constexpr int AHEAD = STAGES - 1;  // tiles loaded ahead of the one being computed
+#pragma unroll
+      for (int s = 0; s < AHEAD; ++s)
+        if (s < KT) direct_load(smem + s * LDS_STAGE, A, lda, rows, B, (int64_t)s * BK);
+      if (KT - 1 >= AHEAD - 1) wait_loads<(AHEAD - 1) * LOADS_PER_STAGE>();
+      else wait_loads<0>();
+      lds_barrier();
+      Frags f0, f1;
+      load_group(smem, 0, f0);
+      int cur = 0;      // stage of tile kt
+      int nxt = AHEAD;  // stage of tile kt + AHEAD (== stage of tile kt - 1)
+      for (int64_t kt = 0; kt < KT; ++kt) {
+        const int cstage = cur;
+        cur = cur + 1 == STAGES ? 0 : cur + 1;
+        load_group(smem + cstage * LDS_STAGE, 1, f1);
+        mfma_group(acc, f0);
+        if (kt + 1 < KT) {
+          // tile kt+1 landed once at most min(AHEAD-2, KT-2-kt) later tiles remain in flight
+          if (KT - 2 - kt >= AHEAD - 2) wait_loads<(AHEAD - 2) * LOADS_PER_STAGE>();
+          else wait_loads<0>();
+          // Publishes tile kt+1.  Every wave passed the MFMAs of tile kt-1 (which consumed all
+          // reads of its stage), so that stage may now be refilled.
+          raw_barrier();
+          if (kt + AHEAD < KT)
+            direct_load(smem + nxt * LDS_STAGE, A, lda, rows, B, (kt + AHEAD) * BK);
+          load_group(smem + cur * LDS_STAGE, 0, f0);
+        }
+        mfma_group(acc, f1);
+        nxt = nxt + 1 == STAGES ? 0 : nxt + 1;
+      }
+      lds_barrier();
+    } else if constexpr (DIRECT) {
       (void)a_vec;
       constexpr int AHEAD = STAGES - 1;  // tiles in flight beyond the one being computed
 #pragma unroll
@@ -373,14 +439,14 @@ struct GemmTile {
   }
 
   // Epilogue.  The rounded tile is staged in LDS (row-major, 16-byte chunk k of row r stored
-  // at chunk position k ^ (r & 7) -- masked to the chunks of a row -- so the two
-  // half-wavefronts, 4 rows apart, write disjoint banks) and written to C with 16-byte stores.  SWIGLU: gate / up accumulators of one output sit in
+  // at chunk position k ^ (r & 7), masked to the chunks of a row) and written to C with
+  // 16-byte stores.  SWIGLU: gate / up accumulators of one output sit in
   // blocks (i, j) / (i, j+1) of the same lane; the stored value is
   // round(round(silu(round(g))) * round(u)) and the tile is BN/2 wide.  Otherwise the value is
   // round(acc + bias[col]) (bias may be null: no add).  Ends with a barrier, so the LDS ring
   // is free for the next tile.
   template <bool SWIGLU>
-  __device__ static __forceinline__ void epilogue(char* smem, f32x16_t (&acc)[FM][FN], T* C,
+  __device__ static __forceinline__ void epilogue(char* smem, Acc (&acc)[FM][FN], T* C,
                                                   int64_t ldc, int rows, int cols, const T* bias,
                                                   bool c_vec) {
     constexpr int OUTW = SWIGLU ? BN / 2 : BN;
@@ -426,7 +492,61 @@ struct GemmTile {
     lds_barrier();
   }
 
-  // Tile-local coordinates of accumulator register r of block (i, j) for this lane.
+  // Ping-pong schedule for 8 wavefronts (2 per SIMD) and a 2-stage ring: waves 0-3 (group 0)
+  // and 4-7 (group 1) alternate between a load phase (the fragments of one K group, LDS ->
+  // registers) and a compute phase (that group's MFMAs), group 1 one phase behind, so on every
+  // SIMD one wave feeds the MFMA pipe while the other reads LDS.  With half step j = 2k + q
+  // (tile k, K group q = 64 bytes of K), global phases separated by workgroup barriers are
+  //   P(2j) = group 0 loads j, group 1 computes j-1;  P(2j+1) = group 0 computes j, group 1 loads j.
+  // Tile k+1 goes into the other stage from P(4k) on (group 0 slots at its load of half step
+  // 2k, group 1 slots at its compute of half step 2k-1) and is waited for at the end of
+  // P(4k+3).  Same MFMA order per element as every other schedule.
+  __device__ static __forceinline__ void mainloop_pingpong(char* smem, Acc (&acc)[FM][FN],
+                                                           const T* A, int64_t lda, int64_t rows,
+                                                           const BSource<T>& B, int64_t K) {
+    static_assert(DIRECT && STAGES == 2 && THREADS == 512 && WGM == 2, "8 waves, 2 stages");
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    const int64_t KT = cdiv(K, BK);
+    if (KT == 0) return;
+    const bool lag = threadIdx.x >= 256;  // group 1
+    direct_load(smem, A, lda, rows, B, 0);
+    wait_loads<0>();
+    lds_barrier();  // tile 0 visible
+    if (lag) {
+      if (KT > 1) direct_load(smem + LDS_STAGE, A, lda, rows, B, BK);
+      lds_barrier();  // group 1 starts one phase behind
+    }
+    for (int64_t kt = 0; kt < KT; ++kt) {
+      const char* st = smem + (int)(kt & 1) * LDS_STAGE;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        Frags f;
+        // load phase
+        if (!lag && q == 0 && kt + 1 < KT)
+          direct_load(smem + (int)((kt + 1) & 1) * LDS_STAGE, A, lda, rows, B, (kt + 1) * BK);
+        load_group(st, q, f);
+        if (lag && q == 1) wait_loads<0>();  // group 1's slots of tile kt+1
+        lds_barrier();
+        // compute phase
+        if (lag && q == 1 && kt + 2 < KT)
+          direct_load(smem + (int)(kt & 1) * LDS_STAGE, A, lda, rows, B, (kt + 2) * BK);
+        __builtin_amdgcn_s_setprio(1);
+        mfma_group(acc, f);
+        __builtin_amdgcn_s_setprio(0);
+        if (!lag && q == 1) wait_loads<0>();  // group 0's slots of tile kt+1
+        lds_barrier();
+      }
+    }
+    if (!lag) lds_barrier();  // pairs with group 1's extra barrier
+  }
+
+  // Tile-local coordinates of accumulator register r (0..15) of block (i, j) for this lane:
+  // the 32x32 MFMA result holds row 8*(r/4) + 4*(lane/32) + r%4, column lane%32 of its block.
   __device__ static __forceinline__ int acc_row(int i, int r) {
     const int lane = threadIdx.x & 63;
     const int wm = (threadIdx.x >> 6) / WGN;
