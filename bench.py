@@ -31,6 +31,46 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 M_SWEEP = [2**i for i in range(13)]  # 1 .. 4096
 SHAPES = ((8192, 2048, True), (2048, 8192, False))  # (N, K, bias)
+# HBM bytes per launch of the roofline kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
+# (each scaled by what the counter reads for a copy of known size); written next to the
+# rocprofv3 summary that produced it.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bmm_kernel_bf16_m4096_n8192_k2048_traffic.md")
+
+
+def measured_traffic():
+    """traffic_bytes_per_launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def profile_kernel(which, iters):
+    """Launch only the roofline GEMM (M=4096, N=8192, K=2048, +bias) or a 512 MiB device copy,
+    iters times: the programs the FETCH_SIZE / WRITE_SIZE counter runs observe."""
+    import torch
+
+    if which == "copy":
+        src = torch.ones(512 * 2**20 // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(iters):
+            dst.copy_(src)
+    else:
+        from batch_invariant_ops import linear_batch_invariant
+
+        g = torch.Generator().manual_seed(20)
+        n, k, _ = SHAPES[0]
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        x = torch.randn(max(M_SWEEP), k, generator=g).to(torch.bfloat16).cuda()
+        for _ in range(iters):
+            linear_batch_invariant(x, w, b)
+    torch.cuda.synchronize()
+    print(f"profile-kernel {which}: {iters} launches done", flush=True)
 
 
 def parse():
@@ -41,6 +81,14 @@ def parse():
     p.add_argument("--configs", default=None, help="also run the 5 BASELINE configs, write a JSON report")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument(
+        "--profile-kernel",
+        choices=("gemm", "copy"),
+        default=None,
+        help="only launch the roofline kernel (gemm) or a 512 MiB device copy (copy) --iters "
+        "times, for hardware-counter runs; prints no JSON line",
+    )
+    p.add_argument("--iters", type=int, default=10)
     return p.parse_args()
 
 
@@ -59,10 +107,12 @@ def event_time(fn, iters, stream=None):
 
 
 def cpu_baseline(seconds):
-    """Stock PyTorch CPU F.linear in bf16 -- the reference's own CPU path for this op -- on a
-    bounded sample of the same workload (M = 256 rows, both linears), repeated for ~seconds."""
+    """The CPU oracle's linear (oracle.linear: fp64 accumulation, one rounding to bf16 -- the
+    restatement of the reference's GEMM the parity tests check against) on a bounded sample of
+    the same workload: M = 256 rows of both configs[1] linears, repeated for ~seconds."""
     import torch
-    import torch.nn.functional as F
+
+    import oracle
 
     cores = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
@@ -73,14 +123,14 @@ def cpu_baseline(seconds):
     b1 = (torch.randn(8192, generator=g) * 0.02).to(torch.bfloat16)
     w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(torch.bfloat16)
     h = torch.randn(m, 8192, generator=g).to(torch.bfloat16)
-    F.linear(x, w1, b1)
-    F.linear(h, w2)
+    oracle.linear(x, w1, b1)
+    oracle.linear(h, w2)
     flops = 0.0
     reps = 0
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds or reps < 2:
-        F.linear(x, w1, b1)
-        F.linear(h, w2)
+        oracle.linear(x, w1, b1)
+        oracle.linear(h, w2)
         flops += 2 * 2.0 * m * 8192 * 2048
         reps += 1
     dt = time.perf_counter() - t0
@@ -89,8 +139,8 @@ def cpu_baseline(seconds):
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"stock torch {torch.__version__} CPU F.linear bf16 (the reference's CPU path), "
-        f"M=256 rows of both configs[1] linears, {reps} reps in {dt:.1f}s",
+        "sample": f"oracle.linear (torch {torch.__version__} CPU, fp64 accumulate, bf16 rounding) "
+        f"on M=256 rows of both configs[1] linears, {reps} reps in {dt:.1f}s",
     }
 
 
@@ -263,6 +313,9 @@ def main():
             file=sys.stderr,
         )
         sys.exit(2)
+    if args.profile_kernel:
+        profile_kernel(args.profile_kernel, args.iters)
+        return
     import torch
 
     from batch_invariant_ops import linear_batch_invariant
@@ -348,7 +401,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel_ms": round(kernel_ms, 5),
         },
         "cpu_baseline": None,

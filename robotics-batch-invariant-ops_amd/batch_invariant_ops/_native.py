@@ -28,6 +28,8 @@ _STATUS = {
 }
 
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: BOOL}
+# floating dtypes the GEMM / row kernels compute in
+DIRECT_DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 _i = ctypes.c_int
 _l = ctypes.c_int64
@@ -110,8 +112,19 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"batch_invariant_ops kernels do not support {dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(tensor: torch.Tensor) -> int:
+    """Handle of torch's current stream on ``tensor``'s device (the launch stream)."""
+    if _raw_stream is not None:
+        return _raw_stream(tensor.get_device())
     return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def function(name: str):
+    """The bound library entry point ``name`` (the library is loaded on first use)."""
+    return getattr(load(), name)
 
 
 def check(rc: int, what: str) -> None:

@@ -178,12 +178,56 @@ def addmm_batch_invariant(bias, a, b, *, beta=1, alpha=1):
     return product + (bias if beta == 1 else bias * beta)
 
 
+def _linear_direct(input, weight, bias):
+    """``linear`` for the common layout -- contiguous input, weight rows of unit stride, a
+    matching 1-D bias -- straight into ``biops_gemm`` without intermediate views (the decode
+    loop of a policy is bound by per-call host time at small batch).  Returns None when the
+    arguments need the general path."""
+    if not (input.is_cuda and weight.is_cuda and weight.dim() == 2 and input.dim() >= 1):
+        return None
+    dtype = input.dtype
+    code = nat.DIRECT_DTYPES.get(dtype)
+    if code is None or weight.dtype != dtype or not input.is_contiguous() or weight.stride(1) != 1:
+        return None
+    n, k = weight.shape
+    shape = input.shape
+    if shape[-1] != k or k == 0 or n == 0:
+        return None
+    bias_ptr = None
+    if bias is not None:
+        if not (bias.is_cuda and bias.dim() == 1 and bias.dtype == dtype and bias.shape[0] == n
+                and bias.stride(0) == 1):
+            return None
+        bias_ptr = bias.data_ptr()
+    m = input.numel() // k
+    out = torch.empty((*shape[:-1], n), device=input.device, dtype=dtype)
+    if m:
+        rc = _gemm_fn()(code, m, n, k, input.data_ptr(), k, 1, weight.data_ptr(), 1, weight.stride(0),
+                        bias_ptr, out.data_ptr(), n, 1, nat.stream_of(out))
+        if rc:
+            nat.check(rc, "biops_gemm")
+    return out
+
+
+_gemm = None
+
+
+def _gemm_fn():
+    global _gemm
+    if _gemm is None:
+        _gemm = nat.function("biops_gemm")
+    return _gemm
+
+
 def linear_batch_invariant(input, weight, bias=None):
     """Batch-invariant ``aten::linear`` for arbitrary leading dimensions.
 
     Reference: linear_batch_invariant (batch_invariant_ops.py:1608-1616): leading dims flatten
     into GEMM rows; ``weight.T`` is read in place (unit stride in K).
     """
+    out = _linear_direct(input, weight, bias)
+    if out is not None:
+        return out
     assert input.ndim >= 1, "linear input must have at least one dimension"
     assert weight.ndim == 2, "linear weight must be a matrix"
     assert input.shape[-1] == weight.shape[-1], "Incompatible dimensions"

@@ -4,6 +4,7 @@
 #include <atomic>
 
 #include "gemm.h"
+#include "gemm_skinny.h"
 
 namespace biops {
 
@@ -34,9 +35,41 @@ BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false)
 BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false)
 #undef BIOPS_CFG
 constexpr int kNumCfg = 12;
+// Entry 12: the skinny tile (gemm_skinny.h), one 32x32 block per workgroup with loader
+// wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
+// back to the automatic choice.
+constexpr int kSkinnyCfg = kNumCfg;
+constexpr int kMenuSize = kNumCfg + 1;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
 // Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
+// Tile t of a launch -> batch indices and the tile's first row / column.  Tiles are numbered
+// batch-major; inside one GEMM, 8 tile-rows form a group walked column by column.
+struct TileOrigin {
+  uint32_t b1, b2;
+  int64_t m0, n0;
+};
+__device__ __forceinline__ TileOrigin tile_origin(const BmmArgs& args, uint32_t t, int BM, int cols) {
+  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
+  const uint32_t tpb = tiles_m * tiles_n;
+  const uint32_t nb2 = (uint32_t)args.nb2;
+  const uint32_t b = t / tpb;
+  const uint32_t in_b = t - b * tpb;
+  const uint32_t per_group = 8u * tiles_n;
+  const uint32_t group = in_b / per_group;
+  const uint32_t first = group * 8u;
+  const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
+  const uint32_t in_group = in_b - group * per_group;
+  const uint32_t tn = in_group / gsize;
+  const uint32_t tm = first + (in_group - tn * gsize);
+  TileOrigin o;
+  o.b1 = b / nb2;
+  o.b2 = b - o.b1 * nb2;
+  o.m0 = (int64_t)tm * BM;
+  o.n0 = (int64_t)tn * cols;
+  return o;
+}
+
 // SwiGLU C = round(round(silu(round(g))) * round(u)) -- the roundings of F.silu(gate) * up
 // applied to rounded bmm outputs -- where gate and up accumulators of one output sit in
 // adjacent 32-column MFMA blocks of the same wavefront.
@@ -48,22 +81,9 @@ __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* 
   constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
   typename Tile::Acc acc[Tile::FM][Tile::FN];
 
-  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
-  const uint32_t tpb = tiles_m * tiles_n;
-  const uint32_t nb2 = (uint32_t)args.nb2, gB = (uint32_t)args.gB;
-  const uint32_t b = t / tpb;
-  const uint32_t in_b = t - b * tpb;
-  // grouped order: 8 tile-rows form a group walked column by column
-  const uint32_t per_group = 8u * tiles_n;
-  const uint32_t group = in_b / per_group;
-  const uint32_t first = group * 8u;
-  const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
-  const uint32_t in_group = in_b - group * per_group;
-  const uint32_t tn = in_group / gsize;
-  const uint32_t tm = first + (in_group - tn * gsize);
-  const uint32_t b1 = b / nb2;
-  const uint32_t b2 = b - b1 * nb2;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * kCols;
+  const TileOrigin o = tile_origin(args, t, BM, kCols);
+  const uint32_t b1 = o.b1, b2 = o.b2, gB = (uint32_t)args.gB;
+  const int64_t m0 = o.m0, n0 = o.n0;
 
   const T* A = reinterpret_cast<const T*>(args.A) + b1 * args.sA1 + b2 * args.sA2 + m0 * args.lda;
   const int64_t boff = b1 * args.sB1 + (b2 / gB) * args.sB2 + (BKM ? n0 * args.ldb : n0);
@@ -107,6 +127,37 @@ void bmm_kernel(BmmArgs args) {
   }
 }
 
+// One 32x32 block per workgroup; wavefront 0 stores it straight from the accumulators with the
+// rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
+template <typename T, int AR>
+__global__ __launch_bounds__(64 * (AR / 8 + 4)) void skinny_kernel(BmmArgs args) {
+  using S = SkinnyTile<T, AR>;
+  static_assert(S::THREADS == 64 * (AR / 8 + 4), "launch bounds");
+  __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
+  const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
+  if (t >= (uint32_t)args.total) return;
+  const TileOrigin o = tile_origin(args, t, 32, 32);
+  const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
+  const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
+               (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
+  const int64_t rows64 = args.M - o.m0, cols64 = args.N - o.n0;
+  const int rows = rows64 < 32 ? (int)rows64 : 32;
+  const int cols = cols64 < 32 ? (int)cols64 : 32;
+  const f32x16_t acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
+  if ((threadIdx.x >> 6) != 0) return;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 31;
+  if (col >= cols) return;
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0 + col;
+  const T* bias = reinterpret_cast<const T*>(args.bias);
+  const float bv = bias ? Num<T>::load(bias + o.n0 + col) : 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (row < rows) Num<T>::store(Cp + (int64_t)row * args.ldc, bias ? acc[r] + bv : acc[r]);
+  }
+}
+
 // -------------------------------------------------------------- tile selection ----
 // Measured full-chip throughput of each entry on large bf16 problems (TFLOP/s, MI355X).  A
 // compute unit works through ceil(tiles / CUs) tiles, each costing BM x BN / throughput (two
@@ -132,9 +183,15 @@ static int forced_cfg() {
   return v;
 }
 
-static int pick_cfg(int dtype, const BmmArgs& a, int epi) {
+// The skinny entry (one workgroup per compute unit, one 32x32 block each) wins when all its
+// blocks run in one round: measured on MI355X at K = 2048 / 8192 it takes 0.6-0.75x the time
+// of the best table entry for up to one block per compute unit and loses beyond (every extra
+// round re-streams the weights).
+
+static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
   if (epi == kEpiSwiglu) return 2;
   const int forced = forced_cfg();
+  if (forced == kSkinnyCfg && skinny_ok) return forced;
   if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7 || forced == 9)))
     return forced;
   const int cus = device_cus();
@@ -147,7 +204,29 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi) {
     const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / kCfgRate[c];
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
+  if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
   return best;
+}
+
+template <typename T, int AR>
+static int launch_skinny_rows(const BmmArgs& a0, hipStream_t stream) {
+  BmmArgs a = a0;
+  a.tiles_m = cdiv(a.M, 32);
+  a.tiles_n = cdiv(a.N, 32);
+  a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
+  if (a.total == 0) return BIOPS_OK;
+  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  hipLaunchKernelGGL((skinny_kernel<T, AR>), dim3((unsigned)a.total), dim3(SkinnyTile<T, AR>::THREADS),
+                     0, stream, a);
+  return check_launch("skinny_kernel");
+}
+
+// A rows loaded per stage: the fewest of 8 / 16 / 32 that hold a block's rows.
+template <typename T>
+static int launch_skinny(const BmmArgs& a, hipStream_t stream) {
+  if (a.M <= 8) return launch_skinny_rows<T, 8>(a, stream);
+  if (a.M <= 16) return launch_skinny_rows<T, 16>(a, stream);
+  return launch_skinny_rows<T, 32>(a, stream);
 }
 
 template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
@@ -194,6 +273,7 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 9: if constexpr (sizeof(T) == 2) return launch_layout<T, 9, EPI>(a, b_kmajor, direct, s); break;
       case 10: return launch_layout<T, 10, EPI>(a, b_kmajor, direct, s);
       case 11: return launch_layout<T, 11, EPI>(a, b_kmajor, direct, s);
+      case kSkinnyCfg: return launch_skinny<T>(a, s);
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);
@@ -217,7 +297,8 @@ int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream)
   // multiple of the 128-byte step.
   const bool direct = b_kmajor && a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) &&
                       !(getenv("BIOPS_GEMM_NO_DIRECT"));
-  const int cfg = pick_cfg(dtype, a, epi);
+  const bool skinny_ok = direct && epi != kEpiSwiglu;
+  const int cfg = pick_cfg(dtype, a, epi, skinny_ok);
   switch (dtype) {
     case BIOPS_F32:
       return epi == kEpiSwiglu ? launch_typed<float, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
@@ -397,10 +478,10 @@ extern "C" int biops_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void
   return launch_bmm(dtype, a, bias ? kEpiBias : kEpiPlain, kmajor, (hipStream_t)stream);
 }
 
-extern "C" int biops_gemm_tile_count(void) { return kNumCfg; }
+extern "C" int biops_gemm_tile_count(void) { return kMenuSize; }
 
 extern "C" int biops_set_gemm_tile(int cfg) {
-  if (cfg < -1 || cfg >= kNumCfg) return fail(BIOPS_ERR_ARG, "tile entry %d outside [-1, %d)", cfg, kNumCfg);
+  if (cfg < -1 || cfg >= kMenuSize) return fail(BIOPS_ERR_ARG, "tile entry %d outside [-1, %d)", cfg, kMenuSize);
   g_forced_cfg.store(cfg, std::memory_order_relaxed);
   return BIOPS_OK;
 }
