@@ -104,10 +104,10 @@ int biops_gemm_tile_count(void);
 /* Force GEMM tile entry `cfg` for every later GEMM/BMM launch in the process (-1 restores the
  * automatic choice, which is the default; the BIOPS_GEMM_CFG environment variable sets the
  * initial value).  Entries 0, 7 and 9 have no fp32 kernel and fall back to the automatic
- * choice for fp32; entry 12 (one 32x32 block per workgroup with loader wavefronts, for few
- * rows) needs K-major B, 16-byte aligned rows and K a multiple of 128 bytes and falls back to
- * the automatic choice elsewhere.  For tuning and for the cross-entry bitwise tests.  No
- * reference counterpart. */
+ * choice for fp32; entries 12 (one 32x32 block per workgroup with loader wavefronts, for few
+ * rows) and 13 (256x256 blocks on four wavefronts, 16-bit types only) need K-major B, 16-byte
+ * aligned rows and K a multiple of 128 bytes and fall back to the automatic choice elsewhere.
+ * For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
 int biops_set_gemm_tile(int cfg);
 
 /* --------------------------------------------------------------- row reductions ---- */

@@ -4,6 +4,7 @@
 #include <atomic>
 
 #include "gemm.h"
+#include "gemm_big.h"
 #include "gemm_skinny.h"
 
 namespace biops {
@@ -39,7 +40,12 @@ constexpr int kNumCfg = 12;
 // wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
 // back to the automatic choice.
 constexpr int kSkinnyCfg = kNumCfg;
-constexpr int kMenuSize = kNumCfg + 1;
+// Entry 13: the large-tile schedule (gemm_big.h), 256x256 blocks on four wavefronts (one per
+// SIMD, accumulators in the accumulation registers).  16-bit operands, direct-load conditions
+// and a plain / bias epilogue; elsewhere it falls back to the automatic choice.  It measures
+// within a few percent of entry 0 and is not chosen automatically (forced entries only).
+constexpr int kBigCfg = kNumCfg + 1;
+constexpr int kMenuSize = kNumCfg + 2;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
 // Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
@@ -158,6 +164,27 @@ __global__ __launch_bounds__(64 * (AR / 8 + 4)) void skinny_kernel(BmmArgs args)
   }
 }
 
+template <typename T, int BM, int BN, int SB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void big_kernel(BmmArgs args) {
+  using Tile = BigTile<T, BM, BN, SB>;
+  __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
+  const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
+  if (t >= (uint32_t)args.total) return;
+  const TileOrigin o = tile_origin(args, t, BM, BN);
+  const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
+  const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
+               (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
+  const int64_t rows64 = args.M - o.m0, cols64 = args.N - o.n0;
+  const int rows = rows64 < BM ? (int)rows64 : BM;
+  const int cols = cols64 < BN ? (int)cols64 : BN;
+  typename Tile::Acc acc[Tile::FM][Tile::FN];
+  Tile::mainloop(smem, acc, A, args.lda, rows, B, args.ldb, cols, args.K);
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0;
+  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + o.n0 : nullptr;
+  Tile::epilogue(smem, acc, Cp, args.ldc, rows, cols, bias, args.c_vec != 0);
+}
+
 // -------------------------------------------------------------- tile selection ----
 // Measured full-chip throughput of each entry on large bf16 problems (TFLOP/s, MI355X).  A
 // compute unit works through ceil(tiles / CUs) tiles, each costing BM x BN / throughput (two
@@ -192,6 +219,8 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
   if (epi == kEpiSwiglu) return 2;
   const int forced = forced_cfg();
   if (forced == kSkinnyCfg && skinny_ok) return forced;
+  const bool big_ok = skinny_ok && dtype != BIOPS_F32;
+  if (forced == kBigCfg && big_ok) return forced;
   if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7 || forced == 9)))
     return forced;
   const int cus = device_cus();
@@ -222,6 +251,18 @@ static int launch_skinny_rows(const BmmArgs& a0, hipStream_t stream) {
 }
 
 // A rows loaded per stage: the fewest of 8 / 16 / 32 that hold a block's rows.
+template <typename T, int BM, int BN, int SB>
+static int launch_big(const BmmArgs& a0, hipStream_t stream) {
+  BmmArgs a = a0;
+  a.tiles_m = cdiv(a.M, BM);
+  a.tiles_n = cdiv(a.N, BN);
+  a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
+  if (a.total == 0) return BIOPS_OK;
+  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  hipLaunchKernelGGL((big_kernel<T, BM, BN, SB>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
+  return check_launch("big_kernel");
+}
+
 template <typename T>
 static int launch_skinny(const BmmArgs& a, hipStream_t stream) {
   if (a.M <= 8) return launch_skinny_rows<T, 8>(a, stream);
@@ -274,6 +315,7 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 10: return launch_layout<T, 10, EPI>(a, b_kmajor, direct, s);
       case 11: return launch_layout<T, 11, EPI>(a, b_kmajor, direct, s);
       case kSkinnyCfg: return launch_skinny<T>(a, s);
+      case kBigCfg: if constexpr (sizeof(T) == 2) return launch_big<T, 256, 256, 128>(a, s); break;
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);

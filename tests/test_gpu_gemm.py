@@ -183,6 +183,7 @@ def tile_menu():
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize(("m", "k", "n", "layout"), (
     (300, 2048, 520, "w"),      # K-major B (nn.Linear), direct-to-LDS loads
+    (512, 256, 768, "w"),       # whole 256x256 blocks (large-tile entry) and 32x32 blocks
     (129, 200, 136, "w"),       # K not a multiple of the step: register path
     (77, 1024, 256, "rowmajor"),  # N-major B
     (33, 65, 47, "w"),          # unaligned rows
