@@ -9,6 +9,8 @@
 // row's position, or whether the row was read once (kept in registers) or several times.
 #pragma once
 
+#include <type_traits>
+
 #include "biops_common.h"
 
 namespace biops {
@@ -64,8 +66,12 @@ __device__ __forceinline__ void store_row_chunk(T* row, int64_t cols, int64_t c0
     } else {
       uint32_t w[N / 2];
 #pragma unroll
-      for (int d = 0; d < N / 2; ++d)
-        w[d] = (uint32_t)Num<T>::to_bits(v[2 * d]) | ((uint32_t)Num<T>::to_bits(v[2 * d + 1]) << 16);
+      for (int d = 0; d < N / 2; ++d) {
+        if constexpr (std::is_same<T, bf16_t>::value)
+          w[d] = f32x2_to_bf16x2_bits(v[2 * d], v[2 * d + 1]);
+        else
+          w[d] = (uint32_t)Num<T>::to_bits(v[2 * d]) | ((uint32_t)Num<T>::to_bits(v[2 * d + 1]) << 16);
+      }
       if constexpr (N == 8) {
         u32x4_t o = {w[0], w[1], w[2], w[3]};
         *reinterpret_cast<u32x4_t*>(row + c0) = o;
@@ -81,12 +87,14 @@ __device__ __forceinline__ void store_row_chunk(T* row, int64_t cols, int64_t c0
     if (c0 + e < cols) Num<T>::store(row + c0 + e, v[e]);
 }
 
-// exp used by the softmax family: the accurate libm expf when the result is stored as fp32,
-// the hardware exp2-based __expf when it is rounded to 16 bits anyway.
+// exp(x - shift) for the softmax family: the accurate libm expf when the result is stored as
+// fp32; when it is rounded to 16 bits anyway, the hardware exp2 of fma(x, log2 e, -shift log2 e)
+// (`shl2e` = shift * log2 e, computed once per row).
+constexpr float kLog2e = 1.4426950408889634f;
 template <typename Tout>
-__device__ __forceinline__ float soft_exp(float x) {
-  if constexpr (sizeof(Tout) == 4) return expf(x);
-  else return __expf(x);
+__device__ __forceinline__ float soft_exp(float x, float shift, float shl2e) {
+  if constexpr (sizeof(Tout) == 4) return expf(x - shift);
+  else return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -shl2e));
 }
 
 // ------------------------------------------------------------------ softmax rows ----
@@ -160,6 +168,7 @@ __device__ __forceinline__ void softmax_row(const Tin* in, Tout* out, int64_t co
   mx = wave_max(mx);
   const bool all_neg_inf = (mx == -INFINITY);
   const float shift = (MODE == kLogSoftmax || !all_neg_inf) ? mx : 0.f;
+  const float shl2e = shift * kLog2e;
 
   float sum = 0.f;
   if (fits) {
@@ -169,7 +178,7 @@ __device__ __forceinline__ void softmax_row(const Tin* in, Tout* out, int64_t co
       if (ci < nchunks) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float ex = (MODE != kLogSoftmax && all_neg_inf) ? 0.f : soft_exp<Tout>(cache[j][e] - shift);
+          const float ex = (MODE != kLogSoftmax && all_neg_inf) ? 0.f : soft_exp<Tout>(cache[j][e], shift, shl2e);
           if (MODE != kLogSoftmax) cache[j][e] = ex;
           if (ci * VEC + e < cols) sum += ex;
         }
@@ -182,7 +191,7 @@ __device__ __forceinline__ void softmax_row(const Tin* in, Tout* out, int64_t co
       transform_chunk<Tin, MODE>(ar, ci * VEC, cols, v);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float ex = (MODE != kLogSoftmax && all_neg_inf) ? 0.f : soft_exp<Tout>(v[e] - shift);
+        const float ex = (MODE != kLogSoftmax && all_neg_inf) ? 0.f : soft_exp<Tout>(v[e], shift, shl2e);
         if (ci * VEC + e < cols) sum += ex;
       }
     }
@@ -232,8 +241,107 @@ __device__ __forceinline__ void softmax_row(const Tin* in, Tout* out, int64_t co
         float o[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
-          o[e] = zero ? 0.f : soft_exp<Tout>(all_neg_inf ? -INFINITY : v[e] - shift) * inv;
+          o[e] = zero ? 0.f : (all_neg_inf ? 0.f : soft_exp<Tout>(v[e], shift, shl2e)) * inv;
         store_row_chunk<Tout, VEC>(out, cols, ci * VEC, vout, o);
+      }
+    }
+  }
+}
+
+// Softmax / log-softmax of R rows (row r at in + r*ld_in) by one wavefront when a row has at
+// most 64*NC chunks (NC <= kRowRegChunks): the loads of all R rows are issued before the first
+// reduction, so a wavefront keeps R*NC chunks per lane in flight.  Per row, the arithmetic and
+// reduction order are those of softmax_row.  Rows r >= nrows are skipped.
+template <typename Tin, typename Tout, int MODE, int R, int NC>
+__device__ __forceinline__ void softmax_rows_fit(const Tin* in, int64_t ld_in, Tout* out, int64_t ld_out,
+                                                 int nrows, int64_t cols, bool vin, bool vout) {
+  static_assert(MODE != kAttn, "plain rows only");
+  static_assert(NC <= kRowRegChunks, "register cache");
+  constexpr int VEC = 16 / sizeof(Tin);
+  const int lane = threadIdx.x & 63;
+  const int64_t nchunks = cdiv(cols, VEC);
+  float cache[R][NC][VEC];
+  // rows past nrows are treated as all -inf and never stored
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t ci = lane + 64 * j;
+      if (r < nrows && ci < nchunks) {
+        load_row_chunk<Tin>(in + r * ld_in, cols, ci * VEC, vin, -INFINITY, cache[r][j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) cache[r][j][e] = -INFINITY;
+      }
+    }
+  }
+  // The butterflies of the R rows run step by step together (independent shuffles overlap).
+  float mx[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    mx[r] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) mx[r] = fmaxf(mx[r], cache[r][j][e]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < R; ++r) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off, 64));
+  float sum[R];
+  bool neg_inf[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    neg_inf[r] = (mx[r] == -INFINITY);
+    const float shift = (MODE == kLogSoftmax || !neg_inf[r]) ? mx[r] : 0.f;
+    const float shl2e = shift * kLog2e;
+    sum[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t ci = lane + 64 * j;
+      if (ci < nchunks) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float ex = (MODE != kLogSoftmax && neg_inf[r]) ? 0.f : soft_exp<Tout>(cache[r][j][e], shift, shl2e);
+          if (MODE != kLogSoftmax) cache[r][j][e] = ex;
+          if (ci * VEC + e < cols) sum[r] += ex;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < R; ++r) sum[r] += __shfl_xor(sum[r], off, 64);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r >= nrows) continue;
+    Tout* orow = out + r * ld_out;
+    if (MODE == kLogSoftmax) {
+      const float lse = logf(sum[r]);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t ci = lane + 64 * j;
+        if (ci < nchunks) {
+          float o[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = cache[r][j][e] - mx[r] - lse;
+          store_row_chunk<Tout, VEC>(orow, cols, ci * VEC, vout, o);
+        }
+      }
+    } else {
+      const bool zero = (sum[r] == 0.f);
+      const float inv = zero ? 0.f : 1.0f / sum[r];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t ci = lane + 64 * j;
+        if (ci < nchunks) {
+          float o[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = zero ? 0.f : cache[r][j][e] * inv;
+          store_row_chunk<Tout, VEC>(orow, cols, ci * VEC, vout, o);
+        }
       }
     }
   }

@@ -1,4 +1,6 @@
 // Softmax / log-softmax and mean / L2-norm reductions.
+#include <type_traits>
+
 #include "rowops.h"
 
 namespace biops {
@@ -11,6 +13,9 @@ struct SoftmaxArgs {
   int32_t vin, vout;
 };
 
+// One wavefront per row for long rows.  Rows of at most 64*NC chunks (NC = 1, 2, 4 per lane):
+// kFitChunks/NC rows per wavefront, whose loads are all issued before the first reduction.
+// Same arithmetic per row either way.
 template <typename Tin, typename Tout, int MODE>
 __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
   const int64_t r = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
@@ -21,8 +26,37 @@ __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
                                a.vout != 0, ar);
 }
 
+constexpr int kFitChunks = 4;  // R * NC: chunks per lane of one wavefront's rows (>= 4, the largest NC)
+
+template <typename Tin, typename Tout, int MODE, int NC>
+__global__ __launch_bounds__(256) void softmax_fit_kernel(SoftmaxArgs a) {
+  constexpr int R = kFitChunks / NC;
+  const int64_t r = ((int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6)) * R;
+  if (r >= a.rows) return;
+  const int n = a.rows - r < R ? (int)(a.rows - r) : R;
+  softmax_rows_fit<Tin, Tout, MODE, R, NC>(reinterpret_cast<const Tin*>(a.in) + r * a.ld_in, a.ld_in,
+                                           reinterpret_cast<Tout*>(a.out) + r * a.ld_out, a.ld_out, n,
+                                           a.cols, a.vin != 0, a.vout != 0);
+}
+
+template <typename Tin, typename Tout, int NC>
+static int launch_softmax_fit(const SoftmaxArgs& a, int is_log, hipStream_t s) {
+  const int64_t blocks = cdiv(a.rows, kRowWaves * (kFitChunks / NC));
+  if (blocks > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "too many rows");
+  if (is_log)
+    hipLaunchKernelGGL((softmax_fit_kernel<Tin, Tout, kLogSoftmax, NC>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((softmax_fit_kernel<Tin, Tout, kSoftmax, NC>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return check_launch("softmax_fit_kernel");
+}
+
 template <typename Tin, typename Tout>
 static int launch_softmax(const SoftmaxArgs& a, int is_log, hipStream_t s) {
+  constexpr int VEC = 16 / (int)sizeof(Tin);
+  const int64_t nchunks = cdiv(a.cols, VEC);
+  if (nchunks <= 64) return launch_softmax_fit<Tin, Tout, 1>(a, is_log, s);
+  if (nchunks <= 128) return launch_softmax_fit<Tin, Tout, 2>(a, is_log, s);
+  if (nchunks <= 256) return launch_softmax_fit<Tin, Tout, 4>(a, is_log, s);
   const int64_t blocks = cdiv(a.rows, kRowWaves);
   if (blocks > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "too many rows");
   if (is_log)
@@ -43,7 +77,8 @@ struct ReduceArgs {
   const void* in;
   void* out;
   int64_t M, N, K, sM, sN, sK;
-  int32_t vin;
+  int32_t vin;   // contiguous rows are 16-byte aligned
+  int32_t kvec;  // K > 1: k contiguous and every (m, n) row start 16-byte aligned
 };
 
 template <int OP>
@@ -98,27 +133,82 @@ __global__ __launch_bounds__(256) void reduce_rows_block(ReduceArgs a) {
   }
 }
 
-// Strided reduction (K > 1): a workgroup owns 64 consecutive k of one m; wavefront w adds the
-// elements n = w, w+4, w+8, ... in increasing n, and the four partials are added as
-// (p0 + p1) + (p2 + p3).  Depends on N only.
-template <typename Tin, typename Tout, int OP>
+// Strided reduction (K > 1): a workgroup owns 64*VK consecutive k of one m (VK consecutive k
+// per lane: 16 bytes when the k run is contiguous and aligned, else 1); wavefront w adds the
+// elements n = w, w+4, w+8, ... of each of its columns in increasing n, and the four partials
+// are added as (p0 + p1) + (p2 + p3).  Depends on N only (VK only decides how columns are
+// grouped into loads).  The loads of kUnroll consecutive n of a wavefront are issued before
+// their additions, which still happen in increasing n.
+constexpr int kStridedUnroll = 8;
+
+template <typename Tin, int VK>
+__device__ __forceinline__ void load_k_run(const Tin* p, int64_t sK, int valid, float (&v)[VK]) {
+  if constexpr (VK > 1) {
+    if (valid >= VK) {
+      const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(p);
+      if constexpr (sizeof(Tin) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(raw[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = Num<Tin>::from_bits((raw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VK; ++e) v[e] = e < valid ? Num<Tin>::load(p + e * sK) : 0.f;
+}
+
+template <typename Tin, typename Tout, int OP, int VK>
 __global__ __launch_bounds__(256) void reduce_strided(ReduceArgs a) {
-  __shared__ float part[4][64];
+  __shared__ float part[4][64 * VK];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const int64_t kblocks = cdiv(a.K, 64);
+  const int64_t kblocks = cdiv(a.K, 64 * VK);
   const int64_t m = blockIdx.x / kblocks;
-  const int64_t k = (blockIdx.x - m * kblocks) * 64 + lane;
-  float acc = 0.f;
-  if (k < a.K) {
-    const Tin* base = reinterpret_cast<const Tin*>(a.in) + m * a.sM + k * a.sK;
-    for (int64_t n = w; n < a.N; n += 4) acc += reduce_term<OP>(Num<Tin>::load(base + n * a.sN));
-  }
-  part[w][lane] = acc;
+  const int64_t k0 = (blockIdx.x - m * kblocks) * 64 * VK + (int64_t)lane * VK;
+  const int valid = k0 < a.K ? (int)(a.K - k0 < VK ? a.K - k0 : VK) : 0;
+  float acc[VK];
+#pragma unroll
+  for (int e = 0; e < VK; ++e) acc[e] = 0.f;
+  // Lanes with a whole k run take a branch-free loop (its loads stay in flight together); the
+  // lanes of a partial run (last workgroup of a row only) take the element-wise one.
+  auto run = [&](auto whole) {
+    constexpr bool WHOLE = decltype(whole)::value;
+    const int nv = WHOLE ? VK : valid;
+    const Tin* base = reinterpret_cast<const Tin*>(a.in) + m * a.sM + k0 * a.sK;
+    int64_t n = w;
+    for (; n + 4 * (kStridedUnroll - 1) < a.N; n += 4 * kStridedUnroll) {
+      float v[kStridedUnroll][VK];
+#pragma unroll
+      for (int u = 0; u < kStridedUnroll; ++u) load_k_run<Tin, VK>(base + (n + 4 * u) * a.sN, a.sK, nv, v[u]);
+#pragma unroll
+      for (int u = 0; u < kStridedUnroll; ++u)
+#pragma unroll
+        for (int e = 0; e < VK; ++e) acc[e] += reduce_term<OP>(v[u][e]);
+    }
+    for (; n < a.N; n += 4) {
+      float v[VK];
+      load_k_run<Tin, VK>(base + n * a.sN, a.sK, nv, v);
+#pragma unroll
+      for (int e = 0; e < VK; ++e) acc[e] += reduce_term<OP>(v[e]);
+    }
+  };
+  if (valid == VK) run(std::true_type{});
+  else if (valid > 0) run(std::false_type{});
+#pragma unroll
+  for (int e = 0; e < VK; ++e) part[w][lane * VK + e] = acc[e];
   __syncthreads();
-  if (w == 0 && k < a.K) {
-    const float s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-    Num<Tout>::store(reinterpret_cast<Tout*>(a.out) + m * a.K + k, reduce_final<OP>(s, a.N));
+  if (w == 0) {
+#pragma unroll
+    for (int e = 0; e < VK; ++e) {
+      if (e < valid) {
+        const int i = lane * VK + e;
+        const float s = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+        Num<Tout>::store(reinterpret_cast<Tout*>(a.out) + m * a.K + k0 + e, reduce_final<OP>(s, a.N));
+      }
+    }
   }
 }
 
@@ -131,10 +221,15 @@ static int launch_reduce(const ReduceArgs& a, hipStream_t s) {
     } else {
       hipLaunchKernelGGL((reduce_rows_block<Tin, Tout, OP>), dim3((unsigned)a.M), dim3(256), 0, s, a);
     }
+  } else if (a.kvec) {
+    constexpr int VK = 16 / (int)sizeof(Tin);
+    const int64_t blocks = a.M * cdiv(a.K, 64 * VK);
+    if (blocks > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "reduction too large");
+    hipLaunchKernelGGL((reduce_strided<Tin, Tout, OP, VK>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   } else {
     const int64_t blocks = a.M * cdiv(a.K, 64);
     if (blocks > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "reduction too large");
-    hipLaunchKernelGGL((reduce_strided<Tin, Tout, OP>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((reduce_strided<Tin, Tout, OP, 1>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   }
   return check_launch("reduce");
 }
@@ -189,8 +284,10 @@ extern "C" int biops_reduce(int op, int dtype_in, int dtype_out, int64_t M, int6
   if (M == 0 || K == 0) return BIOPS_OK;
   if (!in || !out) return fail(BIOPS_ERR_ARG, "null pointer");
   if (K == 1 && sN != 1 && N > 1) return fail(BIOPS_ERR_LAYOUT, "rows must be contiguous when K == 1");
-  ReduceArgs a{in, out, M, N, K, sM, sN, sK, 0};
-  a.vin = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && ((sM * dtype_bytes(dtype_in)) % 16 == 0);
+  ReduceArgs a{in, out, M, N, K, sM, sN, sK, 0, 0};
+  const int elt = dtype_bytes(dtype_in);
+  a.vin = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && ((sM * elt) % 16 == 0);
+  a.kvec = K > 1 && sK == 1 && a.vin && ((sN * elt) % 16 == 0);
   if (M > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "too many rows");
   if (op == BIOPS_REDUCE_L2) {
     BIOPS_DISPATCH_IN_OUT(dtype_in, dtype_out, launch_reduce_op, BIOPS_REDUCE_L2, a, (hipStream_t)stream);
