@@ -136,9 +136,9 @@ void bmm_kernel(BmmArgs args) {
 // One 32x32 block per workgroup; wavefront 0 stores it straight from the accumulators with the
 // rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
 template <typename T, int AR>
-__global__ __launch_bounds__(64 * (AR / 8 + 4)) void skinny_kernel(BmmArgs args) {
+__global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   using S = SkinnyTile<T, AR>;
-  static_assert(S::THREADS == 64 * (AR / 8 + 4), "launch bounds");
+  static_assert(S::THREADS == 512, "launch bounds");
   __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
   const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
   if (t >= (uint32_t)args.total) return;

@@ -4,13 +4,13 @@
 // One workgroup owns one 32x32 output block.  Wavefront 0 computes it with exactly the MFMA
 // sequence of GemmTile (K steps of 128 bytes in order; inside a step chunk pairs q = 0..3, lane
 // half h holding chunk 2q+h), so its bits equal those of every other tile entry.  What differs
-// is how operands arrive: every wavefront of the workgroup -- AR/8 for the A rows and 4 for the
-// 32 B columns -- issues one 16-byte global->LDS chunk load per K step into a ring of 4-6
-// stages of 4 K steps (about 120 KiB).  A stage brings 512 contiguous bytes of every row, and
-// one barrier per stage (not per K step) publishes it: on MI355X the per-step wait + barrier
-// of a 4 KiB step caps a compute unit near 37 GB/s, four-step stages reach ~55 GB/s.  With
-// few rows a block's time is the serial K chain of its accumulator and the weight bytes it
-// streams; the ring keeps the stream ahead of the chain.
+// is how operands arrive: eight wavefronts share the 1 KiB global->LDS load instructions of a
+// stage (8 K steps, 1 KiB of every row) round-robin, into a ring of 2-4 stages (up to the
+// 160 KiB of a compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate grows
+// with the bytes per row per stage and with the number of issuing wavefronts (4 KiB per-step
+// stages on one wavefront: ~37 GB/s; 8-step stages on 8 wavefronts: ~2x).  With few rows a
+// block's time is the serial K chain of its accumulator and the weight bytes it streams; the
+// ring keeps the stream ahead of the chain.
 //
 // Only AR A rows are loaded (AR = 8, 16 or 32, the rows a block can hold); MFMA rows past AR
 // read loaded rows again (row r reads row r mod AR) and, like rows past M, are never stored.
@@ -26,20 +26,21 @@ namespace biops {
 template <typename T, int AR>
 struct SkinnyTile {
   static_assert(AR == 8 || AR == 16 || AR == 32, "A rows per K step");
-  static constexpr int NA = AR / 8;       // wavefronts loading A (8 rows x 8 chunks each)
-  static constexpr int NB = 4;            // wavefronts loading B (32 columns)
-  static constexpr int WAVES = NA + NB;
+  static constexpr int WAVES = 8;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
+  static constexpr int IPK = AR / 8 + 4;                  // 1 KiB load instructions per K step
   static constexpr int LDS_A = AR * kKBytes;             // A rows of one K step
   static constexpr int LDS_KSTEP = LDS_A + 32 * kKBytes;  // one K step: A rows, then B columns
-  static constexpr int U = 4;                             // K steps per stage (even)
+  static constexpr int U = 8;                             // K steps per stage (even)
   static constexpr int LDS_STAGE = U * LDS_KSTEP;
-  static constexpr int STAGES = (128 * 1024) / LDS_STAGE;  // 6 / 5 / 4 for AR = 8 / 16 / 32
+  static constexpr int STAGES = (160 * 1024) / LDS_STAGE;  // 4 / 3 / 2 for AR = 8 / 16 / 32
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
-  static_assert(STAGES >= 3 && (STAGES - 1) * U < 64, "ring depth and vmcnt range");
-  static_assert(U % 2 == 0, "stages start on fragment set 0");
+  static constexpr int LOADS = U * IPK / WAVES;           // per wavefront per stage
+  static_assert(U * IPK % WAVES == 0, "uniform loads per wavefront");
+  static_assert(STAGES >= 2 && STAGES * LOADS < 64, "ring depth and vmcnt range");
+  static_assert(U % 4 == 0, "stages start on fragment set 0");
 
   template <int N>
   __device__ static __forceinline__ void wait_loads() {
@@ -69,25 +70,33 @@ struct SkinnyTile {
 #pragma unroll
     for (int q = 0; q < 4; ++q) Mfma<T>::step(acc, f.a[q], f.b[q]);
   }
-  // One K step on `f` while the next step's fragments are read into `g`.  The reads go out
-  // right after the first MFMA (the wave issues them while that MFMA occupies the pipe) and
-  // have the other three MFMAs to land before the next step needs them.  The scheduling
-  // barriers keep the compiler from sinking each read next to its consumer.
-  __device__ static __forceinline__ void step(f32x16_t& acc, const Frags& f, const char* next, Frags& g) {
-    Mfma<T>::step(acc, f.a[0], f.b[0]);
+  // Two consecutive K steps (their fragments read together).
+  struct Frags2 {
+    Frags s[2];
+  };
+  // K steps j, j+1 on `f` while the fragments of the two steps at `next` are read into `g`.
+  // With an LDS DMA in flight the compiler waits for every outstanding LDS read before an
+  // MFMA that needs one, so the reads go out right after the first MFMA and have the other
+  // seven MFMAs (~250 cycles) to land before the next pair's wait.  The scheduling barriers
+  // keep the compiler from sinking each read next to its consumer.
+  __device__ static __forceinline__ void step2(f32x16_t& acc, const Frags2& f, const char* next, Frags2& g) {
+    Mfma<T>::step(acc, f.s[0].a[0], f.s[0].b[0]);
     __builtin_amdgcn_sched_barrier(0);
-    load_frags(next, g);
+    load_frags(next, g.s[0]);
+    load_frags(next + LDS_KSTEP, g.s[1]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 1; q < 4; ++q) Mfma<T>::step(acc, f.a[q], f.b[q]);
+    for (int q = 1; q < 4; ++q) Mfma<T>::step(acc, f.s[0].a[q], f.s[0].b[q]);
+    mfma(acc, f.s[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
 
   // The 32x32 block at (A, B) with `rows` / `cols` valid rows and columns (>= 1) over KT K
-  // steps.  Stage s holds K steps s*U .. s*U+U-1 (the last stage may hold fewer); each
-  // wavefront issues one chunk load per K step of a stage.  Returns the accumulator in
-  // wavefront 0 (other wavefronts return zeros once their last load is issued; the kernel
-  // only lets wavefront 0 continue).
+  // steps.  Stage s holds K steps s*U .. s*U+U-1 (the last stage may hold fewer).  The U*IPK
+  // 1 KiB load instructions of a stage (K step u, part p: A rows 8p..8p+7 or B columns) are
+  // dealt round-robin to the 8 wavefronts.  Returns the accumulator in wavefront 0 (other
+  // wavefronts return zeros once their last load is issued; the kernel only lets wavefront 0
+  // continue).
   __device__ static __forceinline__ f32x16_t run(char* smem, const T* A, int64_t lda, int rows,
                                                  const T* B, int64_t ldb, int cols, int64_t KT) {
     f32x16_t acc;
@@ -96,87 +105,90 @@ struct SkinnyTile {
     if (KT == 0) return acc;
     const int w = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    // This thread's chunk of every K step: slot s = 64*wave + lane of the A or B region, row
-    // s/8 at LDS slot s%8, holding logical chunk (s%8) ^ ((row>>1)&7) (the lds_off swizzle).
-    const T* src;
-    int dst;  // byte offset of this wavefront's 64 slots inside a K step
-    {
-      const int j = w < NA ? w : w - NA;
-      const int s = 64 * j + lane;
-      const int r = s >> 3;
-      const int c = (s & 7) ^ ((r >> 1) & 7);
-      if (w < NA) {
-        src = A + (int64_t)(r < rows ? r : rows - 1) * lda + c * VEC;
-        dst = 64 * 16 * j;
-      } else {
-        src = B + (int64_t)(r < cols ? r : cols - 1) * ldb + c * VEC;
-        dst = LDS_A + 64 * 16 * j;
-      }
+    // This thread's load i of a stage: instruction w + WAVES*i = (K step u, part p).  Lane l
+    // writes slot l of the part's 64 slots: row 8*part + l/8, holding logical chunk
+    // (l%8) ^ ((row>>1)&7) (the lds_off swizzle).
+    const T* src[LOADS];
+    int ku[LOADS];   // K step inside the stage
+    int dst[LOADS];  // byte offset of the part inside a stage (wave-uniform)
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int ins = w + WAVES * i;
+      const int u = ins / IPK, p = ins % IPK;
+      const bool is_a = p < AR / 8;
+      const int part = is_a ? p : p - AR / 8;
+      const int r = 8 * part + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      src[i] = is_a ? A + (int64_t)(r < rows ? r : rows - 1) * lda + c * VEC
+                    : B + (int64_t)(r < cols ? r : cols - 1) * ldb + c * VEC;
+      ku[i] = u;
+      dst[i] = u * LDS_KSTEP + (is_a ? 0 : LDS_A) + part * 64 * 16;
     }
     const int64_t NS = (KT + U - 1) / U;  // stages
+    // Loads of stage `stage`; K steps past the end re-load the last one (into slots nobody
+    // reads), so every stage issues the same loads and the vmcnt waits are constants.
     auto issue = [&](int64_t stage) {
-      char* buf = smem + (int)(stage % STAGES) * LDS_STAGE + dst;
-      const int64_t k0 = stage * U;
-      if (k0 + U <= KT) {
+      char* buf = smem + (int)(stage % STAGES) * LDS_STAGE;
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-          __builtin_amdgcn_global_load_lds((global_cvoid_t*)(src + (k0 + u) * BK),
-                                           (lds_void_t*)(buf + u * LDS_KSTEP), 16, 0, 0);
-      } else {
-        for (int64_t k = k0; k < KT; ++k)
-          __builtin_amdgcn_global_load_lds((global_cvoid_t*)(src + k * BK),
-                                           (lds_void_t*)(buf + (int)(k - k0) * LDS_KSTEP), 16, 0, 0);
+      for (int i = 0; i < LOADS; ++i) {
+        const int64_t k = stage * U + ku[i];
+        __builtin_amdgcn_global_load_lds((global_cvoid_t*)(src[i] + (k < KT ? k : KT - 1) * BK),
+                                         (lds_void_t*)(buf + dst[i]), 16, 0, 0);
       }
     };
 
-    for (int64_t s = 0; s < NS && s < STAGES; ++s) issue(s);
-    // Stage 0 landed once the loads of stages 1 .. STAGES-1 are all that remain in flight
-    // (exact while those are full stages; otherwise wait for everything).
-    if (NS > STAGES) wait_loads<(STAGES - 1) * U>();
-    else wait_loads<0>();
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) issue(s);
+    wait_loads<(STAGES - 1) * LOADS>();  // stage 0 landed
     lds_barrier();
     // Stages 0 .. NS-2 are full (U steps) and each ends with the barrier that publishes the next
     // stage; the last stage (1..U steps) has none.  Wavefront 0 and the loader wavefronts run
     // separate branch-free loops that meet at the same barriers.
     if (w != 0) {
       for (int64_t s = 0; s + 1 < NS; ++s) {
-        if (s + STAGES < NS) wait_loads<(STAGES - 2) * U>();
-        else wait_loads<0>();
+        wait_loads<(STAGES - 2) * LOADS>();  // stage s+1 landed
         lds_barrier();
-        if (s + STAGES < NS) issue(s + STAGES);
+        issue(s + STAGES);
       }
+      wait_loads<0>();
       return acc;
     }
-    // Two fragment sets used alternately (K step j of a stage reads set j&1 while the next
-    // step's fragments land in the other): copying fragments between registers would stall on
-    // the MFMAs still reading them.  U is even, so every stage starts on set 0.
-    Frags F[2];
-    load_frags(smem, F[0]);
+    // Two fragment sets of two K steps each, used alternately (steps 2d, 2d+1 of a stage read
+    // set d&1 while the next pair lands in the other): copying fragments between registers
+    // would stall on the MFMAs still reading them.  U is a multiple of 4, so every stage
+    // starts on set 0.
+    Frags2 F[2];
+    load_frags(smem, F[0].s[0]);
+    load_frags(smem + LDS_KSTEP, F[0].s[1]);
     for (int64_t s = 0; s + 1 < NS; ++s) {
       const char* cur = smem + (int)(s % STAGES) * LDS_STAGE;
 #pragma unroll
-      for (int j = 0; j + 1 < U; ++j) step(acc, F[j & 1], cur + (j + 1) * LDS_KSTEP, F[(j + 1) & 1]);
-      // Stage s+1 landed once the loads of stages s+2 .. s+STAGES-1 remain in flight.
-      if (s + STAGES < NS) wait_loads<(STAGES - 2) * U>();
-      else wait_loads<0>();
-      // Publishes stage s+1.  Every fragment of stage s is in registers (the last step's were
+      for (int d = 0; d + 1 < U / 2; ++d) step2(acc, F[d & 1], cur + (2 * d + 2) * LDS_KSTEP, F[(d + 1) & 1]);
+      // Stage s+1 landed once the loads of the STAGES-2 later stages remain in flight.
+      wait_loads<(STAGES - 2) * LOADS>();
+      // Publishes stage s+1.  Every fragment of stage s is in registers (the last pair's were
       // read before this barrier), so stage s is refilled.
       lds_barrier();
-      if (s + STAGES < NS) issue(s + STAGES);
-      step(acc, F[(U - 1) & 1], smem + (int)((s + 1) % STAGES) * LDS_STAGE, F[0]);
+      issue(s + STAGES);
+      step2(acc, F[(U / 2 - 1) & 1], smem + (int)((s + 1) % STAGES) * LDS_STAGE, F[0]);
     }
     {
+      // last stage: 1..U steps, fragments read one step ahead (set 0 holds steps 0 and 1)
       const int64_t s = NS - 1;
       const char* cur = smem + (int)(s % STAGES) * LDS_STAGE;
       const int nk = (int)(KT - s * U);
+      mfma(acc, F[0].s[0]);
+      if (nk > 1) mfma(acc, F[0].s[1]);
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
+      for (int j = 2; j < U; ++j) {
         if (j < nk) {
-          if (j + 1 < nk) load_frags(cur + (j + 1) * LDS_KSTEP, F[(j + 1) & 1]);
-          mfma(acc, F[j & 1]);
+          Frags g;
+          load_frags(cur + j * LDS_KSTEP, g);
+          mfma(acc, g);
         }
       }
     }
+    wait_loads<0>();
     return acc;
   }
 };
