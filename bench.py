@@ -277,7 +277,8 @@ def run_all():
     }
     del q, k, v
 
-    # C5: dense top-8 SwiGLU MoE, 64 experts
+    # C5: top-8 SwiGLU MoE, 64 experts; sparse evaluation (default) and the dense every-expert one
+    from batch_invariant_ops.moe import _moe
     g = torch.Generator().manual_seed(5)
     hidden = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
     gu = (torch.randn(64, 2048, 1536, generator=g) * 0.02).to(torch.bfloat16).to(dev)
@@ -288,17 +289,23 @@ def run_all():
     wts, sel = wts.to(dev), sel.to(dev)
     gate, up, down = gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2), dn.transpose(1, 2)
 
-    def moe(t0, t1):
-        return bio.deterministic_token_choice_moe(hidden[t0:t1], wts[t0:t1], sel[t0:t1], gate, up, down)
+    def moe(t0, t1, sparse=True):
+        return _moe(hidden[t0:t1], wts[t0:t1], sel[t0:t1], gate, up, down, sparse=sparse)
 
     full = moe(0, 4096)
     c5 = {"bitwise_T1_T256_T4096": _bitwise(moe(0, 1), full[:1]) and _bitwise(moe(0, 256), full[:256])
-          and _bitwise(moe(256, 512), full[256:512])}
+          and _bitwise(moe(256, 512), full[256:512]),
+          "bitwise_sparse_vs_dense_T4096": _bitwise(full, moe(0, 4096, sparse=False))}
+    expert_bytes = 3 * 2048 * 768 * 2
     for t in (1, 256, 4096):
+        touched = int(torch.unique(sel[:t]).numel())
         ms = event_time(lambda: moe(0, t), 3 if t == 4096 else 10)
         c5[f"T{t}_ms"] = ms
+        c5[f"T{t}_route_tflops"] = 6 * 8 * t * 2048 * 768 / (ms * 1e-3) / 1e12
+        c5[f"T{t}_touched_weight_GBs"] = touched * expert_bytes / (ms * 1e-3) / 1e9
+        ms = event_time(lambda: moe(0, t, sparse=False), 3 if t == 4096 else 10)
+        c5[f"T{t}_dense_ms"] = ms
         c5[f"T{t}_dense_tflops"] = 6 * 64 * t * 2048 * 768 / (ms * 1e-3) / 1e12
-        c5[f"T{t}_weight_GBs"] = 64 * 3 * 2048 * 768 * 2 / (ms * 1e-3) / 1e9
     report["C5_moe"] = c5
     report["library"] = nat.lib_version()
     return report

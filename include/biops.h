@@ -203,6 +203,28 @@ int biops_moe(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_
               void* out, int32_t* bad_index,
               void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes for biops_moe_sparse (-1 for experts > 2048 or invalid sizes).  About
+ * tokens*top_k*(hidden + inter) elements plus small route tables. */
+int64_t biops_moe_sparse_workspace_size(int dtype, int64_t tokens, int64_t top_k, int64_t experts,
+                                        int64_t hidden, int64_t inter);
+
+/* The same operator as biops_moe, same arguments and bit-identical output, evaluating only the
+ * selected routes: routes t*k+s are packed by expert (ranks from wavefront ballots, no atomics),
+ * each expert's rows go through the gate/up and down GEMMs as one grouped launch each, and
+ * the slot sum reads the packed rows.  k/E of the dense arithmetic.  Requires experts <= 2048
+ * and a 256-byte aligned workspace of biops_moe_sparse_workspace_size bytes.
+ * Replaces deterministic_token_choice_moe (moe.py:11-92) with the sparse evaluation its
+ * docstring names as having the same semantics (moe.py:35-38). */
+int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,
+                     int64_t top_k,
+                     const void* x, int64_t sx,
+                     const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+                     const void* up, int64_t suE, int64_t suI, int64_t suD,
+                     const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                     const void* weights, int w_dtype, const int64_t* sel,
+                     void* out, int32_t* bad_index,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

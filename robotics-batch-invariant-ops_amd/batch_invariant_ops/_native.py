@@ -69,6 +69,13 @@ _SIGNATURES = {
         + [_p, _l, _l, _l] * 3
         + [_p, _i, _p, _p, _p, _p, _l, _p],
     ),
+    "biops_moe_sparse_workspace_size": (_l, [_i, _l, _l, _l, _l, _l]),
+    "biops_moe_sparse": (
+        _i,
+        [_i, _l, _l, _l, _l, _l, _p, _l]
+        + [_p, _l, _l, _l] * 3
+        + [_p, _i, _p, _p, _p, _p, _l, _p],
+    ),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -24,17 +24,37 @@ def deterministic_token_choice_moe(
     """Top-k SwiGLU MoE without atomic routing or accumulation.
 
     Reference: deterministic_token_choice_moe (moe.py:11-92).  ``gate_weight`` and
-    ``up_weight`` have shape ``(E, I, D)`` and ``down_weight`` ``(E, D, I)``.  Every expert is
-    evaluated for every token with fixed-schedule GEMMs (gate and up in one launch with the
-    SwiGLU epilogue ``round(round(silu(round(g))) * round(u))``, then the down projection);
-    the selected routes are weighted by ``round(routing_weight)`` and summed over the top-k
-    slots left to right with a rounding after every add.  ``workspace`` is accepted for
-    drop-in compatibility and ignored, as in the reference.
+    ``up_weight`` have shape ``(E, I, D)`` and ``down_weight`` ``(E, D, I)``.  Each selected
+    route (token t, slot s) is computed with fixed-schedule GEMMs (gate and up in one launch
+    with the SwiGLU epilogue ``round(round(silu(round(g))) * round(u))``, then the down
+    projection), weighted by ``round(routing_weight)`` and summed over the top-k slots left to
+    right with a rounding after every add.  ``workspace`` is accepted for drop-in
+    compatibility and ignored, as in the reference.
+
+    By default only the selected routes are evaluated: they are packed by expert (ranks from
+    wavefront ballots, no atomics) and each expert multiplies its own rows.  Every GEMM row is
+    computed by the same fixed instruction sequence whatever the other rows are, so the result
+    has the bits of the reference's every-expert evaluation, which ``BIOPS_MOE_DENSE=1``
+    selects (also used above 2048 experts).
 
     Expert indices outside ``[0, E)`` raise ``RuntimeError`` after the kernels ran (the kernels
     never read out of range); set ``BIOPS_MOE_CHECK_INDICES=0`` to skip that host check.
     """
     del workspace
+    return _moe(hidden_states, routing_weights, selected_experts, gate_weight, up_weight, down_weight,
+                sparse=not nat.env_flag("BIOPS_MOE_DENSE", False))
+
+
+def _moe(
+    hidden_states: torch.Tensor,
+    routing_weights: torch.Tensor,
+    selected_experts: torch.Tensor,
+    gate_weight: torch.Tensor,
+    up_weight: torch.Tensor,
+    down_weight: torch.Tensor,
+    sparse: bool,
+) -> torch.Tensor:
+    """deterministic_token_choice_moe with the evaluation chosen explicitly."""
     if hidden_states.ndim != 2:
         raise ValueError(f"hidden_states must have shape (tokens, hidden), got {hidden_states.shape}")
     if routing_weights.ndim != 2 or selected_experts.shape != routing_weights.shape:
@@ -71,11 +91,18 @@ def deterministic_token_choice_moe(
 
     out = torch.empty((token_count, hidden_size), dtype=dtype, device=x.device)
     lib = nat.load()
-    ws_bytes = lib.biops_moe_workspace_size(code, token_count, num_experts, hidden_size, intermediate_size)
+    ws_bytes = -1
+    if sparse:
+        ws_bytes = lib.biops_moe_sparse_workspace_size(
+            code, token_count, top_k, num_experts, hidden_size, intermediate_size)
+    entry = "biops_moe_sparse" if ws_bytes >= 0 else "biops_moe"
+    if ws_bytes < 0:
+        ws_bytes = lib.biops_moe_workspace_size(code, token_count, num_experts, hidden_size, intermediate_size)
+    # torch's caching allocator returns 512-byte aligned blocks (the sparse path needs 256).
     scratch = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=x.device)
     bad = torch.zeros(1, dtype=torch.int32, device=x.device)
     nat.call(
-        "biops_moe",
+        entry,
         code, token_count, num_experts, hidden_size, intermediate_size, top_k,
         x.data_ptr(), x.stride(0),
         gate.data_ptr(), *gate.stride(),

@@ -13,6 +13,15 @@ enum { kEpiPlain = 0, kEpiBias = 1, kEpiSwiglu = 2 };
 // B is K-major (column n at B + n*ldb, K contiguous) or N-major (K row k at B + k*ldb).
 // In SwiGLU mode B holds the gate weights and B2 the up weights (same layout and strides) and
 // N counts output columns (each needs one gate and one up column).
+//
+// Grouped rows (grp != nullptr, nb1 = nb2 = 1): the rows of A and C are split into row groups
+// g, each multiplied by its own B + g*sB1.  The device table grp holds
+//   grp[0]                      number of m-tiles J,
+//   grp[4 + 4j .. 4 + 4j + 2]   {group, first row, end row of the group} of m-tile j,
+// with m-tiles BM rows high (the BM that grouped_tile_rows() returns for the same problem; a
+// group's last m-tile is cut at the group's end row).  grp_rows bounds the rows of all groups
+// together and grp_groups the number of non-empty groups; the launch is sized for the worst
+// case J <= cdiv(grp_rows, BM) + min(grp_groups, grp_rows) and the tiles past J do nothing.
 struct BmmArgs {
   const void* A;
   const void* B;
@@ -23,12 +32,21 @@ struct BmmArgs {
   int64_t lda, ldb, ldc;
   int64_t nb1, nb2, gB;
   int64_t sA1, sA2, sB1, sB2, sC1, sC2;
+  const int32_t* grp;
+  int64_t grp_rows, grp_groups;
   // filled by the launcher
   int64_t tiles_m, tiles_n, total;
   int32_t a_vec, b_vec, c_vec;
 };
 
+constexpr int kGrpHeader = 4;
+constexpr int kGrpStride = 4;
+
 int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream);
+
+// Tile height of the entry launch_bmm picks for a grouped problem whose M is the mean group
+// size (0 on error).
+int grouped_tile_rows(int dtype, BmmArgs a, int epi, bool b_kmajor);
 
 // Packed variable-length attention work list (host and device copies share the layout):
 //   plan[0] items, plan[1] QK^T tiles, plan[2] PV tiles, plan[3] score rows,

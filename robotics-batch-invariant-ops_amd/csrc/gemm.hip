@@ -1,6 +1,7 @@
 // Persistent fixed-schedule GEMM / batched GEMM entry points.
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "gemm.h"
@@ -53,10 +54,31 @@ constexpr int kMenuSize = kNumCfg + 2;
 // batch-major; inside one GEMM, 8 tile-rows form a group walked column by column.
 struct TileOrigin {
   uint32_t b1, b2;
-  int64_t m0, n0;
+  int64_t m0, m_end, n0;
 };
+template <bool GRP = false>
 __device__ __forceinline__ TileOrigin tile_origin(const BmmArgs& args, uint32_t t, int BM, int cols) {
-  const uint32_t tiles_m = (uint32_t)args.tiles_m, tiles_n = (uint32_t)args.tiles_n;
+  const uint32_t tiles_n = (uint32_t)args.tiles_n;
+  if constexpr (GRP) {
+    // Grouped rows: m-tile list from the device table, same 8-row-group walk.
+    const uint32_t tiles_m = (uint32_t)args.grp[0];
+    const uint32_t per_group = 8u * tiles_n;
+    const uint32_t group = t / per_group;
+    const uint32_t first = group * 8u;
+    const uint32_t gsize = tiles_m - first < 8u ? tiles_m - first : 8u;
+    const uint32_t in_group = t - group * per_group;
+    const uint32_t tn = in_group / gsize;
+    const uint32_t tm = first + (in_group - tn * gsize);
+    const int32_t* e = args.grp + kGrpHeader + kGrpStride * tm;
+    TileOrigin o;
+    o.b1 = (uint32_t)e[0];
+    o.b2 = 0;
+    o.m0 = e[1];
+    o.m_end = e[2];
+    o.n0 = (int64_t)tn * cols;
+    return o;
+  }
+  const uint32_t tiles_m = (uint32_t)args.tiles_m;
   const uint32_t tpb = tiles_m * tiles_n;
   const uint32_t nb2 = (uint32_t)args.nb2;
   const uint32_t b = t / tpb;
@@ -72,6 +94,7 @@ __device__ __forceinline__ TileOrigin tile_origin(const BmmArgs& args, uint32_t 
   o.b1 = b / nb2;
   o.b2 = b - o.b1 * nb2;
   o.m0 = (int64_t)tm * BM;
+  o.m_end = args.M;
   o.n0 = (int64_t)tn * cols;
   return o;
 }
@@ -79,7 +102,7 @@ __device__ __forceinline__ TileOrigin tile_origin(const BmmArgs& args, uint32_t 
 // SwiGLU C = round(round(silu(round(g))) * round(u)) -- the roundings of F.silu(gate) * up
 // applied to rounded bmm outputs -- where gate and up accumulators of one output sit in
 // adjacent 32-column MFMA blocks of the same wavefront.
-template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI, bool GRP>
 __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* smem) {
   using C = Cfg<CFG>;
   using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
@@ -87,7 +110,7 @@ __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* 
   constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
   typename Tile::Acc acc[Tile::FM][Tile::FN];
 
-  const TileOrigin o = tile_origin(args, t, BM, kCols);
+  const TileOrigin o = tile_origin<GRP>(args, t, BM, kCols);
   const uint32_t b1 = o.b1, b2 = o.b2, gB = (uint32_t)args.gB;
   const int64_t m0 = o.m0, n0 = o.n0;
 
@@ -100,7 +123,7 @@ __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* 
   src.ncols = args.N - n0;
   src.swiglu = EPI == kEpiSwiglu;
   src.vec_ok = args.b_vec != 0;
-  const int64_t rows = args.M - m0;
+  const int64_t rows = o.m_end - m0;
   const int64_t cols = args.N - n0;
 
   if constexpr (C::pingpong && DIRECT) Tile::mainloop_pingpong(smem, acc, A, args.lda, rows, src, args.K);
@@ -115,7 +138,10 @@ __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* 
 // Persistent entries walk tiles t = slot, slot + G, ... (slot = XCD-aware rank of the
 // workgroup); the large-tile entries run one tile per workgroup (grid = tiles, same XCD-aware
 // order), which keeps their register budget for the accumulators.
-template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
+// GRP (grouped rows): the tile count is only known on the device.  XCD x (workgroups g with
+// g % 8 == x) takes the x-th eighth of the tiles, so the work stays balanced however far the
+// launch's worst-case size overshoots (the launcher makes G a multiple of 8).
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI, bool GRP>
 __global__ __launch_bounds__(Cfg<CFG>::threads)
 __attribute__((amdgpu_waves_per_eu(Cfg<CFG>::waves_per_eu, Cfg<CFG>::waves_per_eu)))
 void bmm_kernel(BmmArgs args) {
@@ -123,13 +149,30 @@ void bmm_kernel(BmmArgs args) {
   using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
   __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
   const uint32_t G = gridDim.x;
-  const uint32_t total = (uint32_t)args.total;
-  if constexpr (C::persist) {
-    for (uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G); t < total; t += G)
-      bmm_tile<T, CFG, BKM, DIRECT, EPI>(args, t, smem);
+  if constexpr (GRP) {
+    const uint32_t total = (uint32_t)args.grp[0] * (uint32_t)args.tiles_n;
+    const uint32_t per = (total + 7u) / 8u;
+    const uint32_t x = blockIdx.x % 8u, stride = G / 8u;
+    if constexpr (C::persist) {
+      for (uint32_t i = blockIdx.x / 8u; i < per; i += stride) {
+        const uint32_t t = x * per + i;
+        if (t >= total) break;
+        bmm_tile<T, CFG, BKM, DIRECT, EPI, true>(args, t, smem);
+      }
+    } else {
+      // One tile per workgroup: the launch covers the worst case, so G / 8 >= per.
+      const uint32_t i = blockIdx.x / 8u, t = x * per + i;
+      if (i < per && t < total) bmm_tile<T, CFG, BKM, DIRECT, EPI, true>(args, t, smem);
+    }
   } else {
-    const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G);
-    if (t < total) bmm_tile<T, CFG, BKM, DIRECT, EPI>(args, t, smem);
+    const uint32_t total = (uint32_t)args.total;
+    if constexpr (C::persist) {
+      for (uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G); t < total; t += G)
+        bmm_tile<T, CFG, BKM, DIRECT, EPI, false>(args, t, smem);
+    } else {
+      const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, G);
+      if (t < total) bmm_tile<T, CFG, BKM, DIRECT, EPI, false>(args, t, smem);
+    }
   }
 }
 
@@ -146,7 +189,7 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
   const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
                (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
-  const int64_t rows64 = args.M - o.m0, cols64 = args.N - o.n0;
+  const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
   const int rows = rows64 < 32 ? (int)rows64 : 32;
   const int cols = cols64 < 32 ? (int)cols64 : 32;
   const f32x16_t acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
@@ -175,7 +218,7 @@ void big_kernel(BmmArgs args) {
   const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
   const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
                (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
-  const int64_t rows64 = args.M - o.m0, cols64 = args.N - o.n0;
+  const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
   const int rows = rows64 < BM ? (int)rows64 : BM;
   const int cols = cols64 < BN ? (int)cols64 : BN;
   typename Tile::Acc acc[Tile::FM][Tile::FN];
@@ -215,21 +258,39 @@ static int forced_cfg() {
 // of the best table entry for up to one block per compute unit and loses beyond (every extra
 // round re-streams the weights).
 
+// Entries with a kernel for this dtype / epilogue / row mode: no fp32 kernel for 0, 7 and 9;
+// the SwiGLU epilogue needs wave tiles of whole 64-column gate/up pairs and is built for 0, 1
+// and 2; grouped rows are built for a short menu (each entry is a separate kernel).
+static bool grouped_cfg(int c, bool swiglu) {
+  return swiglu ? (c == 0 || c == 2) : (c == 0 || c == 2 || c == 4 || c == 6 || c == 11);
+}
+static bool cfg_ok(int dtype, int c, bool swiglu, bool grouped) {
+  if (c < 0 || c >= kNumCfg) return false;
+  if (dtype == BIOPS_F32 && (c == 0 || c == 7 || c == 9)) return false;
+  if (grouped && !grouped_cfg(c, swiglu)) return false;
+  return !swiglu || c <= 2;
+}
+
 static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
-  if (epi == kEpiSwiglu) return 2;
+  const bool swiglu = epi == kEpiSwiglu;
+  const bool grouped = a.grp != nullptr;
   const int forced = forced_cfg();
   if (forced == kSkinnyCfg && skinny_ok) return forced;
   const bool big_ok = skinny_ok && dtype != BIOPS_F32;
   if (forced == kBigCfg && big_ok) return forced;
-  if (forced >= 0 && forced < kNumCfg && !(dtype == BIOPS_F32 && (forced == 0 || forced == 7 || forced == 9)))
-    return forced;
+  if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
   const int64_t batch = a.nb1 * a.nb2;
+  // Grouped rows: groups of the mean size, each ending in a part-filled m-tile.
+  const int64_t groups = std::max<int64_t>(1, std::min(a.grp_groups, a.grp_rows));
+  const int64_t mean = a.grp_rows / groups;
   int best = 2;
   double best_cost = 1e300;
   for (int c = 0; c < kNumCfg; ++c) {
-    if (dtype == BIOPS_F32 && (c == 0 || c == 7 || c == 9)) continue;  // no fp32 kernel
-    const int64_t tiles = batch * cdiv(a.M, kCfgBM[c]) * cdiv(a.N, kCfgBN[c]);
+    if (!cfg_ok(dtype, c, swiglu, grouped)) continue;
+    const int64_t cols = swiglu ? kCfgBN[c] / 2 : kCfgBN[c];
+    const int64_t mt = grouped ? groups * (mean / kCfgBM[c] + 1) : batch * cdiv(a.M, kCfgBM[c]);
+    const int64_t tiles = mt * cdiv(a.N, cols);
     const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / kCfgRate[c];
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
@@ -270,36 +331,62 @@ static int launch_skinny(const BmmArgs& a, hipStream_t stream) {
   return launch_skinny_rows<T, 32>(a, stream);
 }
 
-template <typename T, int CFG, bool BKM, bool DIRECT, int EPI>
+template <typename T, int CFG, bool BKM, bool DIRECT, int EPI, bool GRP>
 static int launch_cfg(const BmmArgs& a0, hipStream_t stream) {
   using C = Cfg<CFG>;
   BmmArgs a = a0;
   constexpr int64_t kCols = EPI == kEpiSwiglu ? C::bn / 2 : C::bn;
-  a.tiles_m = cdiv(a.M, C::bm);
+  constexpr bool grouped = GRP;
+  a.tiles_m = grouped ? cdiv(a.grp_rows, C::bm) + std::min(a.grp_groups, a.grp_rows) : cdiv(a.M, C::bm);
   a.tiles_n = cdiv(a.N, kCols);
-  a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
+  a.total = (grouped ? 1 : a.nb1 * a.nb2) * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int cus = device_cus();
   if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
   int64_t grid = C::persist ? (int64_t)cus * C::per_cu : a.total;
   if (a.total < grid) grid = a.total;
-  hipLaunchKernelGGL((bmm_kernel<T, CFG, BKM, DIRECT, EPI>), dim3((unsigned)grid), dim3(C::threads),
+  if (grouped) grid = (grid + 7) & ~int64_t(7);
+  hipLaunchKernelGGL((bmm_kernel<T, CFG, BKM, DIRECT, EPI, GRP>), dim3((unsigned)grid), dim3(C::threads),
                      0, stream, a);
   return check_launch("bmm_kernel");
 }
 
-template <typename T, int CFG, int EPI>
+template <typename T, int CFG, int EPI, bool GRP = false>
 static int launch_layout(const BmmArgs& a, bool b_kmajor, bool direct, hipStream_t s) {
-  if (!b_kmajor) return launch_cfg<T, CFG, false, false, EPI>(a, s);
-  if (direct) return launch_cfg<T, CFG, true, true, EPI>(a, s);
-  return launch_cfg<T, CFG, true, false, EPI>(a, s);
+  if (!b_kmajor) {
+    if constexpr (sizeof(T) == 2)
+      if (direct) return launch_cfg<T, CFG, false, true, EPI, GRP>(a, s);
+    return launch_cfg<T, CFG, false, false, EPI, GRP>(a, s);
+  }
+  if (direct) return launch_cfg<T, CFG, true, true, EPI, GRP>(a, s);
+  return launch_cfg<T, CFG, true, false, EPI, GRP>(a, s);
+}
+
+template <typename T, int EPI>
+static int launch_grouped_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, hipStream_t s) {
+  constexpr bool kPlain = EPI != kEpiSwiglu;
+  switch (cfg) {
+    case 0: if constexpr (sizeof(T) == 2) return launch_layout<T, 0, EPI, true>(a, b_kmajor, direct, s); break;
+    case 2: return launch_layout<T, 2, EPI, true>(a, b_kmajor, direct, s);
+    case 4: if constexpr (kPlain) return launch_layout<T, 4, EPI, true>(a, b_kmajor, direct, s); break;
+    case 6: if constexpr (kPlain) return launch_layout<T, 6, EPI, true>(a, b_kmajor, direct, s); break;
+    case 11: if constexpr (kPlain) return launch_layout<T, 11, EPI, true>(a, b_kmajor, direct, s); break;
+    default: break;
+  }
+  return fail(BIOPS_ERR_ARG, "no grouped kernel for tile config %d", cfg);
 }
 
 template <typename T, int EPI>
 static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, hipStream_t s) {
   if constexpr (EPI == kEpiSwiglu) {
-    return launch_layout<T, 2, EPI>(a, b_kmajor, direct, s);
+    switch (cfg) {
+      case 0: if constexpr (sizeof(T) == 2) return launch_layout<T, 0, EPI>(a, b_kmajor, direct, s); break;
+      case 1: return launch_layout<T, 1, EPI>(a, b_kmajor, direct, s);
+      case 2: return launch_layout<T, 2, EPI>(a, b_kmajor, direct, s);
+      default: break;
+    }
+    return fail(BIOPS_ERR_ARG, "no SwiGLU kernel for tile config %d", cfg);
   } else {
     switch (cfg) {
       case 0: if constexpr (sizeof(T) == 2) return launch_layout<T, 0, EPI>(a, b_kmajor, direct, s); break;
@@ -322,11 +409,18 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
   }
 }
 
+// BIOPS_GEMM_NO_DIRECT (any value) forces the register load path (read once per process).
+static bool direct_disabled() {
+  static const bool off = getenv("BIOPS_GEMM_NO_DIRECT") != nullptr;
+  return off;
+}
+
 static bool aligned16(const void* p, int64_t ld, int elt) {
   return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ((ld * elt) % 16 == 0);
 }
 
-int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream) {
+// Operand alignment flags and the direct-load condition; returns the tile entry to launch.
+static int prepare_bmm(int dtype, BmmArgs& a, int epi, bool b_kmajor, bool& direct) {
   const int elt = dtype_bytes(dtype);
   a.a_vec = aligned16(a.A, a.lda, elt) && (a.sA1 * elt) % 16 == 0 && (a.sA2 * elt) % 16 == 0;
   bool bv = aligned16(a.B, a.ldb, elt) && (a.sB1 * elt) % 16 == 0 && (a.sB2 * elt) % 16 == 0;
@@ -335,12 +429,43 @@ int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream)
   a.c_vec = aligned16(a.C, a.ldc, elt) && (a.sC1 * elt) % 16 == 0 && (a.sC2 * elt) % 16 == 0;
   if (a.gB <= 0) a.gB = 1;
   if (a.nb2 <= 0) a.nb2 = 1;
-  // Direct global->LDS loads need whole 16-byte chunks: aligned operands, K-major B and K a
-  // multiple of the 128-byte step.
-  const bool direct = b_kmajor && a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) &&
-                      !(getenv("BIOPS_GEMM_NO_DIRECT"));
-  const bool skinny_ok = direct && epi != kEpiSwiglu;
-  const int cfg = pick_cfg(dtype, a, epi, skinny_ok);
+  // Direct global->LDS loads need whole 16-byte chunks: aligned operands, K a multiple of the
+  // 128-byte step, and B K-major or (16-bit types) N-major with N a multiple of 8.
+  direct = a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) && (b_kmajor || (elt == 2 && a.N % 8 == 0)) &&
+           !direct_disabled();
+  // Grouped rows run on the table entries only (the skinny and large-tile kernels take a fixed
+  // tile count from the host); those two read K-major B only.
+  const bool skinny_ok = direct && b_kmajor && epi != kEpiSwiglu && a.grp == nullptr;
+  return pick_cfg(dtype, a, epi, skinny_ok);
+}
+
+int grouped_tile_rows(int dtype, BmmArgs a, int epi, bool b_kmajor) {
+  if (dtype_bytes(dtype) == 0) return 0;
+  bool direct;
+  const int cfg = prepare_bmm(dtype, a, epi, b_kmajor, direct);
+  return cfg >= 0 && cfg < kNumCfg ? kCfgBM[cfg] : 0;
+}
+
+int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream) {
+  bool direct;
+  const int cfg = prepare_bmm(dtype, a, epi, b_kmajor, direct);
+  if (a.grp) {
+    a.nb1 = a.nb2 = a.gB = 1;
+    a.sA1 = a.sA2 = a.sB2 = a.sC1 = a.sC2 = 0;
+    switch (dtype) {
+      case BIOPS_F32:
+        return epi == kEpiSwiglu ? launch_grouped_typed<float, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                                 : launch_grouped_typed<float, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+      case BIOPS_F16:
+        return epi == kEpiSwiglu ? launch_grouped_typed<f16_t, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                                 : launch_grouped_typed<f16_t, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+      case BIOPS_BF16:
+        return epi == kEpiSwiglu ? launch_grouped_typed<bf16_t, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)
+                                 : launch_grouped_typed<bf16_t, kEpiPlain>(a, b_kmajor, direct, cfg, stream);
+      default:
+        return fail(BIOPS_ERR_DTYPE, "unsupported GEMM dtype %d", dtype);
+    }
+  }
   switch (dtype) {
     case BIOPS_F32:
       return epi == kEpiSwiglu ? launch_typed<float, kEpiSwiglu>(a, b_kmajor, direct, cfg, stream)

@@ -101,9 +101,32 @@ struct BSource {
 // (half-row, slot) bank groups, so the MFMA operand reads (ds_read_b128) are conflict-free.
 __device__ __forceinline__ int lds_off(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
 
+// N-major B stage (16-bit types): K row k of the step holds the tile's CPR = BN/8 chunks of 8
+// columns, chunk c at slot c ^ swz(k).  The MFMA fragments are read with the transposing
+// 64-bit LDS read: within each 16-lane group, result lane i gets element i % 4 of the 64-bit
+// words of source lanes 4j + i / 4 (j = 0..3), so source lane s pointing at row k0 + s / 4,
+// column n0 + 4 (s % 4) hands lane i the K values k0..k0+3 of column n0 + i.  A half wavefront
+// reads rows k0..k0+3 x 4 chunks; swz spreads them over 16 distinct 16-byte bank slots.
+template <int CPR>
+__device__ __forceinline__ int nmajor_swz(int k) {
+  if constexpr (CPR >= 16) return (k & 3) << 2;
+  else if constexpr (CPR == 8) return ((k >> 1) & 1) << 2;
+  else return 0;
+}
+template <int CPR>
+__device__ __forceinline__ int lds_off_n(int k, int col) {
+  return k * CPR * 16 + ((((col >> 3) ^ nmajor_swz<CPR>(k))) << 4) + ((col & 7) << 1);
+}
+typedef short tr16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) tr16x4_t lds_tr16x4_t;
+__device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_tr16x4_t*)p));
+}
+
 // Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN 32x32 blocks).
 // STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
-// (A and K-major B, 16-byte aligned, K a multiple of the step); otherwise through registers.
+// (16-byte aligned rows, K a multiple of the step; B K-major, or N-major for 16-bit types with
+// whole 8-column chunks); otherwise through registers.
 template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT>
 struct GemmTile {
   static constexpr int THREADS = 64 * WGM * WGN;
@@ -127,7 +150,8 @@ struct GemmTile {
   static constexpr int BN_LOADS = (BN_BLOCKS + THREADS - 1) / THREADS;
   static constexpr int B_REGS = B_KMAJOR ? B_LOADS : 4 * BN_LOADS;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert(!DIRECT || B_KMAJOR, "direct loads need a K-major B");
+  static_assert(!DIRECT || B_KMAJOR || sizeof(T) == 2, "N-major direct loads: 16-bit types");
+  static constexpr int CPR_N = BN / VEC;  // chunks per K row of an N-major B stage
   static_assert(!DIRECT || (A_SLOTS % THREADS == 0 && B_SLOTS % THREADS == 0), "direct split");
   static_assert(STAGES >= 2, "at least two stages");
   static constexpr int LOADS_PER_STAGE = A_LOADS + B_LOADS;  // direct path, per thread
@@ -262,17 +286,34 @@ struct GemmTile {
                                        (lds_void_t*)(stage + (THREADS * p + wbase) * 16), 16, 0, 0);
     }
     char* Bs = stage + LDS_A;
+    if constexpr (B_KMAJOR) {
 #pragma unroll
-    for (int p = 0; p < B_SLOTS / THREADS; ++p) {
-      const int s = t + THREADS * p;
-      const int r = s >> 3;
-      const int c = (s & 7) ^ ((r >> 1) & 7);
-      int64_t local;
-      const T* base = B.col_base(r, local);
-      if (local >= B.ncols) local = B.ncols - 1;
-      const T* src = base + local * B.ld + k0 + c * VEC;
-      __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
-                                       (lds_void_t*)(Bs + (THREADS * p + wbase) * 16), 16, 0, 0);
+      for (int p = 0; p < B_SLOTS / THREADS; ++p) {
+        const int s = t + THREADS * p;
+        const int r = s >> 3;
+        const int c = (s & 7) ^ ((r >> 1) & 7);
+        int64_t local;
+        const T* base = B.col_base(r, local);
+        if (local >= B.ncols) local = B.ncols - 1;
+        const T* src = base + local * B.ld + k0 + c * VEC;
+        __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
+                                         (lds_void_t*)(Bs + (THREADS * p + wbase) * 16), 16, 0, 0);
+      }
+    } else {
+      // Slot s: K row s / CPR_N, slot s % CPR_N holding chunk (slot) ^ swz(row) of 8 columns;
+      // chunks past the last column re-load the last whole chunk (never stored).
+#pragma unroll
+      for (int p = 0; p < B_SLOTS / THREADS; ++p) {
+        const int s = t + THREADS * p;
+        const int k = s / CPR_N;
+        const int c = (s % CPR_N) ^ nmajor_swz<CPR_N>(k);
+        int64_t local;
+        const T* base = B.col_base(c * VEC, local);
+        if (local >= B.ncols) local = B.ncols - VEC;
+        const T* src = base + (k0 + k) * B.ld + local;
+        __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
+                                         (lds_void_t*)(Bs + (THREADS * p + wbase) * 16), 16, 0, 0);
+      }
     }
   }
 
@@ -285,9 +326,24 @@ struct GemmTile {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       a[i] = *reinterpret_cast<const u32x4_t*>(stage + lds_off(wm * WM + i * 32 + lr, 2 * q + lb));
+    if constexpr (B_KMAJOR || !DIRECT) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
+      for (int j = 0; j < FN; ++j)
+        b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
+    } else {
+      // Lane group g = lane / 16 holds columns 16 (g & 1) .. +15 of the block, K half g >> 1.
+      const int g = lane >> 4, s = lane & 15;
+      const int k = 16 * q + 8 * (g >> 1) + (s >> 2);
+      const int cb = 16 * (g & 1) + 4 * (s & 3);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const char* base = stage + LDS_A;
+        const int col = wn * WN + j * 32 + cb;
+        const u32x2_t lo = lds_read_tr16(base + lds_off_n<CPR_N>(k, col));
+        const u32x2_t hi = lds_read_tr16(base + lds_off_n<CPR_N>(k + 4, col));
+        b[j] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+      }
+    }
   }
 
   // K group g (0, 1) of a step = MFMA steps q = 2g, 2g+1 (64 bytes of K).

@@ -1,16 +1,26 @@
-// Deterministic token-choice top-k SwiGLU mixture of experts (dense expert evaluation).
-//   act[e] = SwiGLU(x . gate_e^T, x . up_e^T)   one fused GEMM launch over all experts
-//   y[e]   = act[e] . down_e^T                  one GEMM launch over all experts
-//   out[t] = fixed left-to-right sum over the top-k slots of round(y[sel[t,s], t] * round(w[t,s]))
-// No atomics anywhere: every output element is written by exactly one thread.
+// Deterministic token-choice top-k SwiGLU mixture of experts.
+//   act = SwiGLU(x . gate_e^T, x . up_e^T)   (one fused GEMM launch)
+//   y   = act . down_e^T                     (one GEMM launch)
+//   out[t] = fixed left-to-right sum over the top-k slots of round(y(t, s) * round(w[t,s]))
+// Dense path (biops_moe): every expert for every token, y[e, t] for all (e, t).
+// Sparse path (biops_moe_sparse): the routes r = t*k + s are packed by expert into consecutive
+// rows and each expert multiplies only its own rows (grouped GEMMs).  Every GEMM output row is
+// computed by the same fixed MFMA sequence whatever the other rows of its launch are, so the
+// sparse y row of route (t, s) has the bits of the dense y[sel[t,s], t] and both paths give
+// identical outputs.
+// No atomics anywhere: route ranks come from wavefront ballots, and every output element is
+// written by exactly one thread.
+#include <algorithm>
+
 #include "gemm.h"
 
 namespace biops {
 
 struct CombineArgs {
-  const void* y;          // [E, T, D]
+  const void* y;          // dense: [E, T, D]; sparse: packed rows [R, D]
   const void* w;          // [T, k]
   const int64_t* sel;     // [T, k]
+  const int32_t* route_row;  // sparse: packed y row of route t*k+s; nullptr for dense
   void* out;              // [T, D]
   int32_t* bad;           // optional error flag
   int64_t T, D, E, k;
@@ -27,9 +37,30 @@ __device__ __forceinline__ float load_weight(const void* w, int wdt, int64_t idx
   }
 }
 
-// One workgroup per token; each thread owns 4 consecutive hidden columns per pass.
+// Element e of a 16-byte chunk of T as fp32, and the reverse (chunk_put fills e in order).
+template <typename T>
+__device__ __forceinline__ float chunk_elem(const u32x4_t& v, int e) {
+  if constexpr (sizeof(T) == 4) return __uint_as_float(v[e]);
+  else return Num<T>::from_bits((v[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+}
+template <typename T>
+__device__ __forceinline__ void chunk_put(u32x4_t& v, int e, float x) {
+  if constexpr (sizeof(T) == 4) {
+    v[e] = __float_as_uint(x);
+  } else {
+    const uint32_t b = Num<T>::to_bits(x);
+    v[e >> 1] = (e & 1) ? (v[e >> 1] | (b << 16)) : b;
+  }
+}
+
+// One workgroup per token.  Vector path (16-byte rows): each thread owns one 16-byte column
+// chunk per pass and keeps the y loads of 8 slots in flight before adding them in slot order;
+// otherwise 4 scalar columns per thread.  Same arithmetic either way:
+//   acc = v_0, acc = round(acc + v_s) for s = 1..k-1, v_s = round(y_s * round(w_s)).
 template <typename T>
 __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
+  constexpr int V = 16 / (int)sizeof(T);
+  constexpr int G = 8;
   const int64_t t = blockIdx.x;
   bool ok = true;
   for (int64_t s = 0; s < a.k; ++s) {
@@ -38,18 +69,58 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   }
   if (!ok && threadIdx.x == 0 && a.bad) *a.bad = 1;
   T* out = reinterpret_cast<T*>(a.out) + t * a.D;
+  const T* ybase = reinterpret_cast<const T*>(a.y);
+  auto row_of = [&](int64_t r) -> int64_t {
+    return a.route_row ? (int64_t)a.route_row[r] : a.sel[r] * a.T + t;
+  };
+  if (a.vec) {
+    for (int64_t d0 = (int64_t)threadIdx.x * V; d0 < a.D; d0 += 256 * V) {
+      float acc[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[e] = 0.f;
+      if (ok) {
+        for (int64_t s0 = 0; s0 < a.k; s0 += G) {
+          u32x4_t v[G];
+          float w[G];
+#pragma unroll
+          for (int u = 0; u < G; ++u) {
+            if (s0 + u < a.k) {
+              const int64_t r = t * a.k + s0 + u;
+              w[u] = load_weight<T>(a.w, a.w_dtype, r);
+              v[u] = *reinterpret_cast<const u32x4_t*>(ybase + row_of(r) * a.D + d0);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < G; ++u) {
+            if (s0 + u < a.k) {
+#pragma unroll
+              for (int e = 0; e < V; ++e) {
+                const float x = Num<T>::round(chunk_elem<T>(v[u], e) * w[u]);
+                acc[e] = (s0 + u == 0) ? x : Num<T>::round(acc[e] + x);
+              }
+            }
+          }
+        }
+      }
+      u32x4_t o = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < V; ++e) chunk_put<T>(o, e, acc[e]);
+      *reinterpret_cast<u32x4_t*>(out + d0) = o;
+    }
+    return;
+  }
   for (int64_t d0 = (int64_t)threadIdx.x * 4; d0 < a.D; d0 += 256 * 4) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     if (ok) {
       for (int64_t s = 0; s < a.k; ++s) {
-        const int64_t e = a.sel[t * a.k + s];
-        const float w = load_weight<T>(a.w, a.w_dtype, t * a.k + s);
-        const T* y = reinterpret_cast<const T*>(a.y) + (e * a.T + t) * a.D;
+        const int64_t r = t * a.k + s;
+        const float w = load_weight<T>(a.w, a.w_dtype, r);
+        const T* y = ybase + row_of(r) * a.D;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           if (d0 + c < a.D) {
-            const float r = Num<T>::round(Num<T>::load(y + d0 + c) * w);
-            acc[c] = (s == 0) ? r : Num<T>::round(acc[c] + r);
+            const float v = Num<T>::round(Num<T>::load(y + d0 + c) * w);
+            acc[c] = (s == 0) ? v : Num<T>::round(acc[c] + v);
           }
         }
       }
@@ -60,10 +131,258 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   }
 }
 
-static bool weight_layout(int64_t sE, int64_t sRow, int64_t sK, int64_t rows, int64_t K, bool& kmajor,
-                          int64_t& ld) {
-  (void)sE;
-  return b_layout(K, rows, sK, sRow, kmajor, ld);
+// ------------------------------------------------------------------ route packing ----
+// Route r = t*k + s belongs to bucket sel[r] (an expert) or, for an index outside [0, E), to
+// bucket E (never computed).  The routes are cut into chunks of `chunk` consecutive routes:
+//   rank kernel  rank[r]      = routes r' < r of r's chunk in r's bucket,
+//                counts[c][b] = routes of chunk c in bucket b;
+//   plan kernel  counts[c][b] -> routes of chunks before c in bucket b (in place),
+//                off[e]       = first packed row of expert e (experts in index order),
+//                grp1 / grp2  = m-tile tables of the two grouped GEMMs;
+//   gather       row(r) = off[e] + counts[c][e] + rank[r], x[t] copied to packed row row(r).
+// Packed rows of an expert are therefore its routes in increasing r.
+constexpr int kRankWaves = 4;
+constexpr int kMaxSparseExperts = 2048;
+constexpr int kPlanThreads = 1024;
+
+struct PackArgs {
+  const int64_t* sel;
+  int32_t* rank;
+  int32_t* counts;     // [S][E + 1]
+  int32_t* off;        // [E + 1]
+  int32_t* grp1;       // m-tiles of bm1 rows
+  int32_t* grp2;       // m-tiles of bm2 rows
+  int32_t* route_row;  // [R], -1 for bucket E
+  const void* x;
+  void* xg;            // [R, D] packed rows
+  int64_t R, k, E, S, chunk, D, sx;
+  int32_t bm1, bm2, elt, vec;
+};
+
+static int64_t route_chunk(int64_t R) {
+  // 1024 routes per chunk, more when that gives over 256 chunks (the plan kernel walks them).
+  const int64_t batches = std::max<int64_t>(16, cdiv(R, int64_t(256) * 64));
+  return 64 * batches;
+}
+
+// One wavefront per chunk, 64 routes at a time: the lanes holding the same bucket find each
+// other through one ballot per bucket-index bit; each lane's rank is the count of such lanes
+// below it plus the bucket's running count, which the group's lowest lane advances.
+__global__ __launch_bounds__(256) void moe_rank_kernel(PackArgs a) {
+  extern __shared__ int32_t hist[];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t E1 = a.E + 1;
+  const int64_t c = (int64_t)blockIdx.x * kRankWaves + w;
+  if (c >= a.S) return;  // whole wavefronts only; no workgroup barrier follows
+  int32_t* h = hist + w * E1;
+  for (int64_t b = lane; b < E1; b += 64) h[b] = 0;
+  const int nbits = 32 - __clz((int)a.E);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int64_t r0 = c * a.chunk;
+  const int64_t r1 = std::min(a.R, r0 + a.chunk);
+  constexpr int NB = 16;  // batches of 64 routes whose selections are loaded together
+  for (int64_t base = r0; base < r1; base += 64 * NB) {
+    int bucket[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t r = base + 64 * u + lane;
+      int b = (int)a.E;
+      if (r < r1) {
+        const int64_t e = a.sel[r];
+        if (e >= 0 && e < a.E) b = (int)e;
+      }
+      bucket[u] = b;
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t r = base + 64 * u + lane;
+      const bool valid = r < r1;
+      const int b = bucket[u];
+      uint64_t same = __ballot(valid);
+      for (int bit = 0; bit < nbits; ++bit) {
+        const bool on = (b >> bit) & 1;
+        const uint64_t m = __ballot(valid && on);
+        same &= on ? m : ~m;
+      }
+      if (valid) {
+        const int32_t run = h[b];
+        const int lower = __popcll(same & below);
+        a.rank[r] = run + lower;
+        if (lower == 0) h[b] = run + __popcll(same);
+      }
+    }
+  }
+  for (int64_t b = lane; b < E1; b += 64) a.counts[c * E1 + b] = h[b];
+}
+
+// One workgroup.  Thread i owns buckets [i*per, (i+1)*per); an exclusive scan over the threads
+// of (rows, bm1 tiles, bm2 tiles) places each expert's rows and m-tiles.
+__global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
+  __shared__ int32_t part[3][kPlanThreads];
+  const int tid = threadIdx.x;
+  const int64_t E = a.E, E1 = E + 1;
+  const int64_t per = (E1 + kPlanThreads - 1) / kPlanThreads;
+  const int64_t b0 = std::min(E1, tid * per), b1 = std::min(E1, b0 + per);
+  int32_t rows = 0, t1 = 0, t2 = 0;
+  for (int64_t b = b0; b < b1; ++b) {
+    int32_t run = 0;
+    int64_t c = 0;
+    for (; c + 4 <= a.S; c += 4) {
+      int32_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = a.counts[(c + u) * E1 + b];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a.counts[(c + u) * E1 + b] = run;
+        run += v[u];
+      }
+    }
+    for (; c < a.S; ++c) {
+      const int32_t v = a.counts[c * E1 + b];
+      a.counts[c * E1 + b] = run;
+      run += v;
+    }
+    a.off[b] = run;  // bucket size for now
+    if (b < E) {
+      rows += run;
+      t1 += (run + a.bm1 - 1) / a.bm1;
+      t2 += (run + a.bm2 - 1) / a.bm2;
+    }
+  }
+  part[0][tid] = rows;
+  part[1][tid] = t1;
+  part[2][tid] = t2;
+  __syncthreads();
+  // Inclusive Hillis-Steele scan over the threads.
+  for (int d = 1; d < kPlanThreads; d <<= 1) {
+    int32_t v0 = 0, v1 = 0, v2 = 0;
+    if (tid >= d) {
+      v0 = part[0][tid - d];
+      v1 = part[1][tid - d];
+      v2 = part[2][tid - d];
+    }
+    __syncthreads();
+    if (tid >= d) {
+      part[0][tid] += v0;
+      part[1][tid] += v1;
+      part[2][tid] += v2;
+    }
+    __syncthreads();
+  }
+  int32_t row0 = part[0][tid] - rows, j1 = part[1][tid] - t1, j2 = part[2][tid] - t2;
+  for (int64_t b = b0; b < b1; ++b) {
+    const int32_t n = a.off[b];
+    a.off[b] = row0;
+    if (b < E) {
+      for (int32_t m = 0; m < n; m += a.bm1, ++j1) {
+        int32_t* g = a.grp1 + kGrpHeader + kGrpStride * j1;
+        g[0] = (int32_t)b; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
+      }
+      for (int32_t m = 0; m < n; m += a.bm2, ++j2) {
+        int32_t* g = a.grp2 + kGrpHeader + kGrpStride * j2;
+        g[0] = (int32_t)b; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
+      }
+      row0 += n;
+    }
+  }
+  if (tid == 0) {
+    a.grp1[0] = part[1][kPlanThreads - 1];
+    a.grp2[0] = part[2][kPlanThreads - 1];
+  }
+}
+
+// One wavefront per route: its packed row, and its token's row of x copied there.
+__global__ __launch_bounds__(256) void moe_gather_kernel(PackArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= a.R) return;
+  const int64_t e = a.sel[r];
+  const bool ok = e >= 0 && e < a.E;
+  int64_t row = -1;
+  if (ok) row = (int64_t)a.off[e] + a.counts[(r / a.chunk) * (a.E + 1) + e] + a.rank[r];
+  if (lane == 0) a.route_row[r] = (int32_t)row;
+  if (!ok) return;
+  const int64_t bytes = a.D * a.elt;
+  const char* src = reinterpret_cast<const char*>(a.x) + (r / a.k) * a.sx * a.elt;
+  char* dst = reinterpret_cast<char*>(a.xg) + row * bytes;
+  if (a.vec) {
+    for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16)
+      *reinterpret_cast<u32x4_t*>(dst + o) = *reinterpret_cast<const u32x4_t*>(src + o);
+  } else {
+    for (int64_t o = (int64_t)lane * 2; o < bytes; o += 64 * 2)
+      *reinterpret_cast<uint16_t*>(dst + o) = *reinterpret_cast<const uint16_t*>(src + o);
+  }
+}
+
+// Workspace of the sparse path (byte offsets, 256-byte aligned).
+struct SparseLayout {
+  int64_t xg, act, rank, route, counts, off, grp1, grp2, total;
+};
+
+static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int64_t I) {
+  auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
+  const int64_t S = cdiv(R, route_chunk(R));
+  // Tile tables sized for the smallest tile height of the menu (32 rows).
+  const int64_t tiles = cdiv(R, 32) + std::min(E, R);
+  SparseLayout L;
+  int64_t p = 0;
+  L.xg = p; p += al(R * D * elt);  // gathered x rows; the down projection then writes y here
+  L.act = p; p += al(R * I * elt);
+  L.rank = p; p += al(R * 4);
+  L.route = p; p += al(R * 4);
+  L.counts = p; p += al(S * (E + 1) * 4);
+  L.off = p; p += al((E + 1) * 4);
+  L.grp1 = p; p += al((kGrpHeader + kGrpStride * tiles) * 4);
+  L.grp2 = p; p += al((kGrpHeader + kGrpStride * tiles) * 4);
+  L.total = p;
+  return L;
+}
+
+static int launch_combine(int dtype, CombineArgs c, hipStream_t s) {
+  if (c.T > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "too many tokens");
+  const int elt = dtype_bytes(dtype);
+  c.vec = (c.D * elt) % 16 == 0 && reinterpret_cast<uintptr_t>(c.y) % 16 == 0 &&
+          reinterpret_cast<uintptr_t>(c.out) % 16 == 0;
+  switch (dtype) {
+    case BIOPS_F32: hipLaunchKernelGGL(moe_combine_kernel<float>, dim3((unsigned)c.T), dim3(256), 0, s, c); break;
+    case BIOPS_F16: hipLaunchKernelGGL(moe_combine_kernel<f16_t>, dim3((unsigned)c.T), dim3(256), 0, s, c); break;
+    default: hipLaunchKernelGGL(moe_combine_kernel<bf16_t>, dim3((unsigned)c.T), dim3(256), 0, s, c); break;
+  }
+  return check_launch("moe_combine_kernel");
+}
+
+// Shared argument checks and the two expert GEMMs' operand layouts.
+struct ExpertGemms {
+  BmmArgs gu, dn;
+  bool gu_kmajor, dn_kmajor;
+};
+
+static int expert_gemms(int64_t tokens, int64_t experts, int64_t hidden, int64_t inter, const void* x,
+                        int64_t sx, const void* gate, int64_t sgE, int64_t sgI, int64_t sgD, const void* up,
+                        int64_t suE, int64_t suI, int64_t suD, const void* down, int64_t sdE, int64_t sdD,
+                        int64_t sdI, ExpertGemms& g) {
+  if (sgE != suE || sgI != suI || sgD != suD)
+    return fail(BIOPS_ERR_LAYOUT, "gate and up weights must share strides");
+  int64_t ldb;
+  // act[., i]: B = gate_e / up_e viewed as [I, D] (column i, K = d).
+  if (!b_layout(hidden, inter, sgD, sgI, g.gu_kmajor, ldb))
+    return fail(BIOPS_ERR_LAYOUT, "gate/up weights need a unit stride");
+  g.gu = BmmArgs{};
+  g.gu.A = x; g.gu.B = gate; g.gu.B2 = up;
+  g.gu.M = tokens; g.gu.N = inter; g.gu.K = hidden;
+  g.gu.lda = sx; g.gu.ldb = ldb;
+  g.gu.nb1 = experts; g.gu.nb2 = 1; g.gu.gB = 1;
+  g.gu.sB1 = sgE;
+  // y[., d] = act[., :] . down_e[d, :]
+  if (!b_layout(inter, hidden, sdI, sdD, g.dn_kmajor, ldb))
+    return fail(BIOPS_ERR_LAYOUT, "down weights need a unit stride");
+  g.dn = BmmArgs{};
+  g.dn.B = down;
+  g.dn.M = tokens; g.dn.N = hidden; g.dn.K = inter;
+  g.dn.lda = inter; g.dn.ldb = ldb; g.dn.ldc = hidden;
+  g.dn.nb1 = experts; g.dn.nb2 = 1; g.dn.gB = 1;
+  g.dn.sB1 = sdE;
+  return BIOPS_OK;
 }
 
 }  // namespace biops
@@ -91,8 +410,10 @@ extern "C" int biops_moe(int dtype, int64_t tokens, int64_t experts, int64_t hid
   if (tokens < 0 || experts <= 0 || hidden < 0 || inter < 0 || top_k < 0)
     return fail(BIOPS_ERR_ARG, "invalid MoE sizes");
   if (tokens == 0 || hidden == 0) return BIOPS_OK;
-  if (sgE != suE || sgI != suI || sgD != suD)
-    return fail(BIOPS_ERR_LAYOUT, "gate and up weights must share strides");
+  ExpertGemms g;
+  int rc = expert_gemms(tokens, experts, hidden, inter, x, sx, gate, sgE, sgI, sgD, up, suE, suI, suD, down,
+                        sdE, sdD, sdI, g);
+  if (rc != BIOPS_OK) return rc;
   const int64_t need = biops_moe_workspace_size(dtype, tokens, experts, hidden, inter);
   if (workspace_bytes < need) return fail(BIOPS_ERR_SIZE, "workspace %lld < %lld bytes",
                                           (long long)workspace_bytes, (long long)need);
@@ -102,40 +423,100 @@ extern "C" int biops_moe(int dtype, int64_t tokens, int64_t experts, int64_t hid
   const int64_t act_elems = (experts * tokens * inter + 63) & ~int64_t(63);
   void* act = ws;
   void* y = ws + act_elems * elt;
-  int rc;
 
   if (top_k > 0) {
-    // act[e, t, i] for every expert: B = gate_e / up_e viewed as [I, D] (column i, K = d).
-    bool kmaj;
-    int64_t ldb;
-    if (!weight_layout(sgE, sgI, sgD, inter, hidden, kmaj, ldb))
-      return fail(BIOPS_ERR_LAYOUT, "gate/up weights need a unit stride");
-    BmmArgs g{};
-    g.A = x; g.B = gate; g.B2 = up; g.C = act;
-    g.M = tokens; g.N = inter; g.K = hidden;
-    g.lda = sx; g.ldb = ldb; g.ldc = inter;
-    g.nb1 = experts; g.nb2 = 1; g.gB = 1;
-    g.sA1 = 0; g.sB1 = sgE; g.sC1 = tokens * inter;
-    if ((rc = launch_bmm(dtype, g, kEpiSwiglu, kmaj, s)) != BIOPS_OK) return rc;
-
-    // y[e, t, d] = act[e, t, :] . down_e[d, :]
-    if (!weight_layout(sdE, sdD, sdI, hidden, inter, kmaj, ldb))
-      return fail(BIOPS_ERR_LAYOUT, "down weights need a unit stride");
-    BmmArgs dn{};
-    dn.A = act; dn.B = down; dn.C = y;
-    dn.M = tokens; dn.N = hidden; dn.K = inter;
-    dn.lda = inter; dn.ldb = ldb; dn.ldc = hidden;
-    dn.nb1 = experts; dn.nb2 = 1; dn.gB = 1;
-    dn.sA1 = tokens * inter; dn.sB1 = sdE; dn.sC1 = tokens * hidden;
-    if ((rc = launch_bmm(dtype, dn, kEpiPlain, kmaj, s)) != BIOPS_OK) return rc;
+    // act[e, t, i] and y[e, t, d] for every expert: A broadcast over the experts.
+    g.gu.C = act; g.gu.ldc = inter; g.gu.sA1 = 0; g.gu.sC1 = tokens * inter;
+    if ((rc = launch_bmm(dtype, g.gu, kEpiSwiglu, g.gu_kmajor, s)) != BIOPS_OK) return rc;
+    g.dn.A = act; g.dn.C = y; g.dn.sA1 = tokens * inter; g.dn.sC1 = tokens * hidden;
+    if ((rc = launch_bmm(dtype, g.dn, kEpiPlain, g.dn_kmajor, s)) != BIOPS_OK) return rc;
   }
+  CombineArgs c{y, weights, sel, nullptr, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
+  return launch_combine(dtype, c, s);
+}
 
-  CombineArgs c{y, weights, sel, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
-  if (tokens > 0x7fffffffLL) return fail(BIOPS_ERR_ARG, "too many tokens");
-  switch (dtype) {
-    case BIOPS_F32: hipLaunchKernelGGL(moe_combine_kernel<float>, dim3((unsigned)tokens), dim3(256), 0, s, c); break;
-    case BIOPS_F16: hipLaunchKernelGGL(moe_combine_kernel<f16_t>, dim3((unsigned)tokens), dim3(256), 0, s, c); break;
-    default: hipLaunchKernelGGL(moe_combine_kernel<bf16_t>, dim3((unsigned)tokens), dim3(256), 0, s, c); break;
+extern "C" int64_t biops_moe_sparse_workspace_size(int dtype, int64_t tokens, int64_t top_k,
+                                                   int64_t experts, int64_t hidden, int64_t inter) {
+  const int elt = dtype_bytes(dtype);
+  if (elt == 0 || tokens < 0 || top_k < 0 || experts <= 0 || hidden < 0 || inter < 0) return -1;
+  if (experts > kMaxSparseExperts) return -1;
+  return sparse_layout(elt, tokens * top_k, experts, hidden, inter).total;
+}
+
+extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
+                                int64_t inter, int64_t top_k, const void* x, int64_t sx,
+                                const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+                                const void* up, int64_t suE, int64_t suI, int64_t suD,
+                                const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                                const void* weights, int w_dtype, const int64_t* sel, void* out,
+                                int32_t* bad_index, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  if (!is_float_dtype(dtype) || !is_float_dtype(w_dtype))
+    return fail(BIOPS_ERR_DTYPE, "unsupported MoE dtype");
+  if (tokens < 0 || experts <= 0 || hidden < 0 || inter < 0 || top_k < 0)
+    return fail(BIOPS_ERR_ARG, "invalid MoE sizes");
+  if (experts > kMaxSparseExperts)
+    return fail(BIOPS_ERR_ARG, "sparse MoE supports up to %d experts", kMaxSparseExperts);
+  if (tokens == 0 || hidden == 0) return BIOPS_OK;
+  const int64_t R = tokens * top_k;
+  if (R >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many routes");
+  ExpertGemms g;
+  int rc = expert_gemms(tokens, experts, hidden, inter, x, sx, gate, sgE, sgI, sgD, up, suE, suI, suD, down,
+                        sdE, sdD, sdI, g);
+  if (rc != BIOPS_OK) return rc;
+  const int elt = dtype_bytes(dtype);
+  const SparseLayout L = sparse_layout(elt, R, experts, hidden, inter);
+  if (workspace_bytes < L.total) return fail(BIOPS_ERR_SIZE, "workspace %lld < %lld bytes",
+                                             (long long)workspace_bytes, (long long)L.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(BIOPS_ERR_LAYOUT, "workspace must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = reinterpret_cast<char*>(workspace);
+  int32_t* route_row = reinterpret_cast<int32_t*>(ws + L.route);
+
+  if (R > 0) {
+    // Grouped GEMM operands: packed rows, one row group per expert.
+    g.gu.A = ws + L.xg; g.gu.lda = hidden;
+    g.gu.C = ws + L.act; g.gu.ldc = inter;
+    g.gu.grp = reinterpret_cast<const int32_t*>(ws + L.grp1);
+    g.dn.A = ws + L.act;
+    g.dn.C = ws + L.xg;
+    g.dn.grp = reinterpret_cast<const int32_t*>(ws + L.grp2);
+    for (BmmArgs* b : {&g.gu, &g.dn}) {
+      b->grp_rows = R;
+      b->grp_groups = experts;
+      b->M = cdiv(R, experts);  // mean rows per expert, for the tile choice
+    }
+    const int bm1 = grouped_tile_rows(dtype, g.gu, kEpiSwiglu, g.gu_kmajor);
+    const int bm2 = grouped_tile_rows(dtype, g.dn, kEpiPlain, g.dn_kmajor);
+    if (bm1 < 32 || bm2 < 32) return fail(BIOPS_ERR_ARG, "no grouped GEMM tile");
+
+    PackArgs p{};
+    p.sel = sel;
+    p.rank = reinterpret_cast<int32_t*>(ws + L.rank);
+    p.counts = reinterpret_cast<int32_t*>(ws + L.counts);
+    p.off = reinterpret_cast<int32_t*>(ws + L.off);
+    p.grp1 = reinterpret_cast<int32_t*>(ws + L.grp1);
+    p.grp2 = reinterpret_cast<int32_t*>(ws + L.grp2);
+    p.route_row = route_row;
+    p.x = x;
+    p.xg = ws + L.xg;
+    p.R = R; p.k = top_k; p.E = experts;
+    p.chunk = route_chunk(R);
+    p.S = cdiv(R, p.chunk);
+    p.D = hidden; p.sx = sx;
+    p.bm1 = bm1; p.bm2 = bm2; p.elt = elt;
+    p.vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (sx * elt) % 16 == 0 && (hidden * elt) % 16 == 0;
+    const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
+    hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)cdiv(p.S, kRankWaves)), dim3(256), hist_bytes, s, p);
+    if ((rc = check_launch("moe_rank_kernel")) != BIOPS_OK) return rc;
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
+    if ((rc = check_launch("moe_plan_kernel")) != BIOPS_OK) return rc;
+    hipLaunchKernelGGL(moe_gather_kernel, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, p);
+    if ((rc = check_launch("moe_gather_kernel")) != BIOPS_OK) return rc;
+    if ((rc = launch_bmm(dtype, g.gu, kEpiSwiglu, g.gu_kmajor, s)) != BIOPS_OK) return rc;
+    if ((rc = launch_bmm(dtype, g.dn, kEpiPlain, g.dn_kmajor, s)) != BIOPS_OK) return rc;
   }
-  return check_launch("moe_combine_kernel");
+  CombineArgs c{ws + L.xg, weights, sel, route_row, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
+  return launch_combine(dtype, c, s);
 }

@@ -202,3 +202,27 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
         assert tile_menu.biops_set_gemm_tile(cfg) == 0
         assert_bitwise(matmul_persistent(x, b, bias), ref, f"tile entry {cfg}")
         assert_bitwise(matmul_persistent(x[5:6], b, bias), ref[5:6], f"tile entry {cfg}, one row")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize(("m", "k", "n"), (
+    (300, 2048, 520),   # N-major direct loads, partial last column tile
+    (77, 1024, 256),
+    (1, 64, 8),         # one chunk of columns
+    (130, 128, 1000),   # N % 256 != 0: clamped chunks in the last tile
+    (64, 4096, 24),
+    (513, 192, 264),
+    (40, 256, 100),     # N % 8 != 0: register path
+))
+def test_nmajor_b_matches_kmajor_bits(tile_menu, dtype, m, k, n):
+    """Row-major B (N-major: global->LDS loads and transposing LDS reads when whole 8-column
+    chunks allow) gives the bits of the same values stored K-major, on every tile entry."""
+    x = gpu(randn(m, k, seed=5100 + m, dtype=dtype))
+    b_rows = gpu(randn(k, n, seed=5101 + n, dtype=dtype))
+    b_cols = b_rows.t().contiguous().t()
+    assert b_rows.stride(1) == 1 and b_cols.stride(0) == 1
+    tile_menu.biops_set_gemm_tile(-1)
+    ref = matmul_persistent(x, b_cols)
+    for cfg in range(tile_menu.biops_gemm_tile_count()):
+        assert tile_menu.biops_set_gemm_tile(cfg) == 0
+        assert_bitwise(matmul_persistent(x, b_rows), ref, f"tile entry {cfg}")
