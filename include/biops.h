@@ -130,6 +130,35 @@ int biops_reduce(int op, int dtype_in, int dtype_out, int64_t M, int64_t N, int6
                  const void* in, int64_t sM, int64_t sN, int64_t sK,
                  void* out, void* stream);
 
+/* ---------------------------------------------------------------- convolution ---- */
+
+/* Workspace bytes for biops_conv (same arguments; -1 for invalid sizes, 0 when none is needed). */
+int64_t biops_conv_workspace_size(int dtype, int nd, int transposed, int64_t batch, int64_t cin,
+                                  const int64_t* in_size, int64_t cout, const int64_t* ksize,
+                                  const int64_t* stride, const int64_t* padding,
+                                  const int64_t* dilation, int64_t groups);
+
+/* nd-dimensional convolution (nd = 1, 2, 3), x[B, C_in, *in_size] with element strides
+ * x_strides[nd + 2], out[B, C_out, *out_size] contiguous, bias[C_out] or NULL.  The size arrays
+ * hold nd host values.
+ * Regular (transposed = 0): weight [C_out, C_in/groups, *ksize] contiguous, out_size =
+ * (in + 2 pad - dil (k - 1) - 1) / stride + 1.  Depthwise 1-D (groups = C_in = C_out):
+ * fp32 sum over the taps in order plus the bias, one rounding.  Otherwise each output element
+ * is one fixed-schedule GEMM dot product over (channel, taps) of the group, rounded, then
+ * round(value + bias[c]).
+ * Transposed (transposed = 1): stride == ksize, padding 0, dilation 1 only (non-overlapping);
+ * weight [C_in, C_out/groups, *ksize] contiguous, out_size = in * ksize, spatial input dims
+ * contiguous; one GEMM dot product over the group's input channels per output, rounded, then
+ * round(value + bias[c]).
+ * Replaces depthwise_conv1d_kernel and conv1d/conv2d/conv3d_batch_invariant
+ * (batch_invariant_ops.py:434-780), conv_transpose2d/3d_batch_invariant (783-941) and their
+ * dispatcher convolution_batch_invariant (944-971). */
+int biops_conv(int dtype, int nd, int transposed, int64_t batch, int64_t cin, const int64_t* in_size,
+               int64_t cout, const int64_t* ksize, const int64_t* stride, const int64_t* padding,
+               const int64_t* dilation, int64_t groups,
+               const void* x, const int64_t* x_strides, const void* weight, const void* bias,
+               void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------- attention ---- */
 
 /* Workspace bytes biops_sdpa needs (the materialised score/probability matrices). */

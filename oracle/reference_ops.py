@@ -12,6 +12,7 @@ from __future__ import annotations
 import math
 
 import torch
+import torch.nn.functional as F
 
 __all__ = [
     "rnd",
@@ -26,6 +27,8 @@ __all__ = [
     "sdpa",
     "varlen_sdpa",
     "moe",
+    "conv",
+    "conv_abs",
     "gemm_abs",
     "gamma",
 ]
@@ -209,3 +212,39 @@ def moe(hidden, routing_weights, selected, gate, up, down):
         route = rnd(y[selected[:, s], t_idx] * w[:, s : s + 1], dt)
         out = route if out is None else rnd(out + route, dt)
     return out.to(dt)
+
+
+# -------------------------------------------------------------------- convolution ----
+def _conv_f64(x, w, stride, padding, dilation, transposed, output_padding, groups):
+    nd = x.ndim - 2
+    if transposed:
+        f = {1: F.conv_transpose1d, 2: F.conv_transpose2d, 3: F.conv_transpose3d}[nd]
+        return f(x, w, None, stride, padding, output_padding, groups, dilation)
+    f = {1: F.conv1d, 2: F.conv2d, 3: F.conv3d}[nd]
+    return f(x, w, None, stride, padding, dilation, groups)
+
+
+def conv(x, w, bias, stride, padding, dilation, transposed, output_padding, groups):
+    """aten::convolution with the reference's roundings (BIO 434-971).  Depthwise 1-D
+    (groups == C_in == C_out, one channel per group, BIO 531): the taps and the bias summed in
+    the wide accumulator, one rounding (BIO 435-494).  Every other form goes through bmm_persistent
+    (one rounding of the patch dot products) and then adds the bias as a separate tensor op, which
+    rounds again (BIO 590-595, 675-680, 775-780, 818-826, 898-906)."""
+    dt = x.dtype
+    nd = x.ndim - 2
+    acc = _conv_f64(x.double(), w.double(), stride, padding, dilation, transposed, output_padding, groups)
+    shape = (1, -1) + (1,) * nd
+    depthwise = nd == 1 and not transposed and groups == x.shape[1] == w.shape[0] and w.shape[1] == 1
+    if depthwise:
+        out = acc if bias is None else acc + bias.double().reshape(shape)
+        return out.to(dt)
+    out = rnd(acc, dt)
+    if bias is not None:
+        out = rnd(out + bias.double().reshape(shape), dt)
+    return out.to(dt)
+
+
+def conv_abs(x, w, stride, padding, dilation, transposed, output_padding, groups):
+    """The convolution of |x| and |w| in float64: scales each output's dot-product error bound."""
+    return _conv_f64(x.double().abs(), w.double().abs(), stride, padding, dilation, transposed,
+                     output_padding, groups)

@@ -69,6 +69,8 @@ _SIGNATURES = {
         + [_p, _l, _l, _l] * 3
         + [_p, _i, _p, _p, _p, _p, _l, _p],
     ),
+    "biops_conv_workspace_size": (_l, [_i, _i, _i, _l, _l, _p, _l, _p, _p, _p, _p, _l]),
+    "biops_conv": (_i, [_i, _i, _i, _l, _l, _p, _l, _p, _p, _p, _p, _l, _p, _p, _p, _p, _p, _p, _l, _p]),
     "biops_moe_sparse_workspace_size": (_l, [_i, _l, _l, _l, _l, _l]),
     "biops_moe_sparse": (
         _i,

@@ -12,6 +12,7 @@ workspaces and validates arguments.  There is no CPU path.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import math
 from collections import namedtuple
 from typing import Any
@@ -665,22 +666,162 @@ def varlen_scaled_dot_product_attention_batch_invariant(
 
 
 # ---------------------------------------------------------------- convolutions ----
-def _conv_not_built(name):
-    def fn(*args, **kwargs):
-        raise NotImplementedError(
-            f"{name}: the convolution family is not part of this MI355X build yet "
-            "(aten::convolution is not overridden by set_batch_invariant_mode)"
-        )
-
-    fn.__name__ = name
-    return fn
+def _conv_sizes(values, n, name):
+    values = tuple(int(v) for v in values)
+    if len(values) == 1 and n > 1:
+        return values * n
+    assert len(values) == n, f"{name} must have one or {n} values, got {values!r}"
+    return values
 
 
-conv1d_batch_invariant = _conv_not_built("conv1d_batch_invariant")
-conv2d_batch_invariant = _conv_not_built("conv2d_batch_invariant")
-conv3d_batch_invariant = _conv_not_built("conv3d_batch_invariant")
-conv_transpose2d_batch_invariant = _conv_not_built("conv_transpose2d_batch_invariant")
-conv_transpose3d_batch_invariant = _conv_not_built("conv_transpose3d_batch_invariant")
+def _conv_native(input, weight, bias, nd, transposed, stride, padding, dilation, groups, out_channels,
+                 out_spatial):
+    """One biops_conv call: output [B, out_channels, *out_spatial], fresh and contiguous."""
+    out = torch.empty((input.shape[0], out_channels, *out_spatial), dtype=input.dtype, device=input.device)
+    if out.numel() == 0:
+        return out
+    nat.require_gpu_tensors(input, weight, *(() if bias is None else (bias,)))
+    x = input
+    if transposed and not x[0, 0].is_contiguous():
+        x = x.contiguous()  # the GEMM reads the spatial dims as one contiguous run
+    w = weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+
+    def arr(values):
+        return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+    in_size, ksize = arr(input.shape[2:]), arr(weight.shape[2:])
+    st, pd, dl, xs = arr(stride), arr(padding), arr(dilation), arr(x.stride())
+    code = nat.dtype_code(input.dtype)
+    sizes = (code, nd, int(transposed), input.shape[0], input.shape[1], ctypes.addressof(in_size), out_channels,
+             ctypes.addressof(ksize), ctypes.addressof(st), ctypes.addressof(pd), ctypes.addressof(dl), groups)
+    ws_bytes = int(nat.load().biops_conv_workspace_size(*sizes))
+    if ws_bytes < 0:
+        raise RuntimeError("biops_conv_workspace_size rejected the convolution sizes")
+    workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=input.device)
+    nat.call(
+        "biops_conv", *sizes,
+        x.data_ptr(), ctypes.addressof(xs), w.data_ptr(), 0 if b is None else b.data_ptr(),
+        out.data_ptr(), workspace.data_ptr(), workspace.numel(), nat.stream_of(out),
+    )
+    return out
+
+
+def _regular_conv(nd, input, weight, bias, stride, padding, dilation, transposed, output_padding, groups):
+    """Shared argument rules of the regular 1-D / 2-D / 3-D convolutions (batch_invariant_ops.py
+    :505-514, 609-618, 695-704)."""
+    names = {1: "1-D", 2: "2-D", 3: "3-D"}
+    assert input.ndim == nd + 2 and weight.ndim == nd + 2, f"only {names[nd]} convolution is supported"
+    assert not transposed, "transposed convolution is not supported"
+    assert all(value == 0 for value in output_padding), (
+        f"output_padding requires transposed convolution, got {output_padding!r}"
+    )
+    assert input.dtype == weight.dtype and (bias is None or bias.dtype == input.dtype), "Incompatible dtypes"
+    assert input.shape[1] == weight.shape[1] * groups, "Incompatible channel dimensions"
+    assert weight.shape[0] % groups == 0, "output channels must be divisible by groups"
+    if nd == 1:
+        stride, padding, dilation = (tuple(stride), tuple(padding), tuple(dilation))
+        for values, name in ((stride, "stride"), (padding, "padding"), (dilation, "dilation")):
+            assert len(values) == 1, f"{name} must have one value, got {values!r}"
+    stride = _conv_sizes(stride, nd, "stride")
+    padding = _conv_sizes(padding, nd, "padding")
+    dilation = _conv_sizes(dilation, nd, "dilation")
+    kernel = weight.shape[2:]
+    out_spatial = tuple(
+        (input.shape[2 + i] + 2 * padding[i] - dilation[i] * (kernel[i] - 1) - 1) // stride[i] + 1
+        for i in range(nd)
+    )
+    return _conv_native(input, weight, bias, nd, False, stride, padding, dilation, groups, weight.shape[0],
+                        out_spatial)
+
+
+def conv1d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed, output_padding, groups):
+    """Batch-invariant 1-D convolution (reference conv1d_batch_invariant, batch_invariant_ops.py
+    :497-595).  Depthwise (groups == C_in == C_out, one channel per group, 531): fp32 sum over the
+    taps in order plus the bias, one rounding, like the reference's dedicated kernel (434-494).
+    Every other group layout: one fixed-schedule GEMM dot product over (channel, tap) per output,
+    rounded, then the bias added and rounded (the reference's bmm + add, 565-595)."""
+    return _regular_conv(1, input, weight, bias, stride, padding, dilation, transposed, output_padding, groups)
+
+
+def conv2d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed, output_padding, groups):
+    """Batch-invariant 2-D convolution (reference conv2d_batch_invariant, batch_invariant_ops.py
+    :598-682): per-output GEMM dot products over (channel, kh, kw) of the group (im2col), grouped
+    and dilated convolution included, bias added after the GEMM rounding."""
+    return _regular_conv(2, input, weight, bias, stride, padding, dilation, transposed, output_padding, groups)
+
+
+def conv3d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed, output_padding, groups):
+    """Batch-invariant 3-D convolution (reference conv3d_batch_invariant, batch_invariant_ops.py
+    :685-780), as conv2d with (kd, kh, kw) taps."""
+    return _regular_conv(3, input, weight, bias, stride, padding, dilation, transposed, output_padding, groups)
+
+
+def _transposed_conv(nd, input, weight, bias, stride, padding, dilation, output_padding, groups):
+    """Non-overlapping transposed convolution (reference 783-941): stride == kernel, no padding,
+    output padding or dilation, so every output position receives one contribution."""
+    names = {2: "2-D", 3: "3-D"}
+    assert input.ndim == nd + 2 and weight.ndim == nd + 2, f"only {names[nd]} convolution is supported"
+    assert input.dtype == weight.dtype and (bias is None or bias.dtype == input.dtype), "Incompatible dtypes"
+    assert input.shape[1] == weight.shape[0], "Incompatible input channels"
+    assert input.shape[1] % groups == 0, "input channels must be divisible by groups"
+    stride = _conv_sizes(stride, nd, "stride")
+    padding = _conv_sizes(padding, nd, "padding")
+    dilation = _conv_sizes(dilation, nd, "dilation")
+    output_padding = _conv_sizes(output_padding, nd, "output_padding")
+    kernel = tuple(weight.shape[2:])
+    label = "ConvTranspose2d" if nd == 2 else "ConvTranspose3d"
+    assert stride == kernel, (
+        f"batch-invariant {label} currently requires non-overlapping "
+        f"stride == kernel_size, got stride={stride}, kernel_size={kernel}"
+    )
+    zeros = (0,) * nd
+    assert padding == zeros, f"padding is not supported, got {padding}"
+    assert output_padding == zeros, f"output_padding is not supported, got {output_padding}"
+    assert dilation == (1,) * nd, f"dilation is not supported, got {dilation}"
+    out_channels = weight.shape[1] * groups
+    if bias is not None:
+        assert bias.shape == (out_channels,), "Incompatible bias shape"
+    out_spatial = tuple(input.shape[2 + i] * kernel[i] for i in range(nd))
+    return _conv_native(input, weight, bias, nd, True, stride, padding, dilation, groups, out_channels,
+                        out_spatial)
+
+
+def conv_transpose2d_batch_invariant(input, weight, bias, stride, padding, dilation, output_padding, groups):
+    """Batch-invariant non-overlapping 2-D transposed convolution (reference
+    conv_transpose2d_batch_invariant, batch_invariant_ops.py:783-861): one GEMM dot product over
+    the group's input channels per output element, rounded, then the bias added and rounded."""
+    return _transposed_conv(2, input, weight, bias, stride, padding, dilation, output_padding, groups)
+
+
+def conv_transpose3d_batch_invariant(input, weight, bias, stride, padding, dilation, output_padding, groups):
+    """Batch-invariant non-overlapping 3-D transposed convolution (reference
+    conv_transpose3d_batch_invariant, batch_invariant_ops.py:864-941)."""
+    return _transposed_conv(3, input, weight, bias, stride, padding, dilation, output_padding, groups)
+
+
+def convolution_batch_invariant(input, weight, bias, stride, padding, dilation, transposed, output_padding,
+                                groups):
+    """aten::convolution dispatch to the supported forms (batch_invariant_ops.py:944-971)."""
+    if input.ndim == 3 and weight.ndim == 3:
+        return conv1d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed,
+                                      output_padding, groups)
+    if input.ndim == 4 and weight.ndim == 4 and transposed:
+        return conv_transpose2d_batch_invariant(input, weight, bias, stride, padding, dilation,
+                                                output_padding, groups)
+    if input.ndim == 4 and weight.ndim == 4:
+        return conv2d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed,
+                                      output_padding, groups)
+    if input.ndim == 5 and weight.ndim == 5 and transposed:
+        return conv_transpose3d_batch_invariant(input, weight, bias, stride, padding, dilation,
+                                                output_padding, groups)
+    if input.ndim == 5 and weight.ndim == 5:
+        return conv3d_batch_invariant(input, weight, bias, stride, padding, dilation, transposed,
+                                      output_padding, groups)
+    raise AssertionError(
+        f"only 1-D, 2-D and 3-D convolution are supported, got input rank {input.ndim} "
+        f"and weight rank {weight.ndim}"
+    )
 
 
 # ------------------------------------------------------------ mode / registration ----
@@ -695,6 +836,7 @@ _OVERRIDES = (
     ("aten::addmm", addmm_batch_invariant),
     ("aten::linear", linear_batch_invariant),
     ("aten::bmm", bmm_batch_invariant),
+    ("aten::convolution", convolution_batch_invariant),
     ("aten::scaled_dot_product_attention", scaled_dot_product_attention_batch_invariant),
     ("aten::_softmax", _softmax_batch_invariant),
     ("aten::_log_softmax", _log_softmax_batch_invariant),

@@ -54,8 +54,44 @@ def test_public_api_matches_reference_surface():
     assert set(bio.__all__) == REFERENCE_API
     assert bio.__version__ == "0.2.0"
     assert bio.get_batch_invariant_attention_block_size() == bio.AttentionBlockSize(16, 16)
-    with pytest.raises(NotImplementedError):
-        bio.conv2d_batch_invariant(torch.zeros(1))
+
+
+def test_conv_argument_rules_need_no_gpu():
+    """The reference's conv assertions (batch_invariant_ops.py:505-514, 609-618, 795-832) fire on
+    the host; valid CPU tensors are refused (no CPU path)."""
+    x, w = torch.randn(2, 4, 9, 9), torch.randn(6, 2, 3, 3)
+    with pytest.raises(AssertionError, match="only 2-D convolution"):
+        bio.conv2d_batch_invariant(x[0], w, None, (1,), (0,), (1,), False, (0,), 2)
+    with pytest.raises(AssertionError, match="transposed convolution is not supported"):
+        bio.conv2d_batch_invariant(x, w, None, (1,), (0,), (1,), True, (0,), 2)
+    with pytest.raises(AssertionError, match="output_padding requires transposed"):
+        bio.conv2d_batch_invariant(x, w, None, (1,), (0,), (1,), False, (1, 0), 2)
+    with pytest.raises(AssertionError, match="Incompatible dtypes"):
+        bio.conv2d_batch_invariant(x, w.double(), None, (1,), (0,), (1,), False, (0,), 2)
+    with pytest.raises(AssertionError, match="Incompatible channel dimensions"):
+        bio.conv2d_batch_invariant(x, w, None, (1,), (0,), (1,), False, (0,), 1)
+    with pytest.raises(AssertionError, match="must have one value"):
+        bio.conv1d_batch_invariant(x[:, :, 0], w[:, :, 0], None, (1, 1), (0,), (1,), False, (0,), 2)
+    with pytest.raises(AssertionError, match="non-overlapping"):
+        bio.conv_transpose2d_batch_invariant(x, torch.randn(4, 3, 3, 3), None, (2, 2), (0, 0), (1, 1), (0, 0), 1)
+    from batch_invariant_ops.batch_invariant_ops import convolution_batch_invariant
+
+    with pytest.raises(AssertionError, match="only 1-D, 2-D and 3-D"):
+        convolution_batch_invariant(x[0, 0], w[0, 0], None, (1,), (0,), (1,), False, (0,), 1)
+    with pytest.raises(ValueError):
+        bio.conv2d_batch_invariant(x, w, None, (1,), (0,), (1,), False, (0,), 2)  # CPU tensors
+    L = lib()
+    import ctypes
+    arr = lambda *v: (ctypes.c_int64 * len(v))(*v)  # noqa: E731
+    sizes = [arr(9, 9), arr(3, 3), arr(1, 1), arr(0, 0), arr(1, 1)]
+    ptrs = [ctypes.addressof(a) for a in sizes]
+    # regular 2-D, bf16: padded weights [6, 64] then patches [2 * 2 * 49, 64]
+    ws = L.biops_conv_workspace_size(2, 2, 0, 2, 4, ptrs[0], 6, ptrs[1], ptrs[2], ptrs[3], ptrs[4], 2)
+    assert ws == 6 * 64 * 2 + 2 * 2 * 49 * 64 * 2
+    # transposed requires stride == kernel
+    assert L.biops_conv_workspace_size(2, 2, 1, 2, 4, ptrs[0], 6, ptrs[1], ptrs[2], ptrs[3], ptrs[4], 2) == -1
+    # groups must divide the channels
+    assert L.biops_conv_workspace_size(2, 2, 0, 2, 4, ptrs[0], 6, ptrs[1], ptrs[2], ptrs[3], ptrs[4], 3) == -1
 
 
 def test_host_validation_needs_no_gpu():
@@ -170,17 +206,20 @@ def test_mode_context_is_exception_safe_and_reentrant():
 
 
 def test_mode_registers_gpu_key_only():
-    """The overrides live on dispatch key CUDA (ROCm GPUs); CPU tensors keep the stock kernels."""
+    """The ten overrides of the reference (batch_invariant_ops.py:1668-1684) live on dispatch key
+    CUDA (ROCm GPUs); CPU tensors keep the stock kernels."""
     a = torch.randn(4, 5)
     b = torch.randn(5, 3)
     with bio.set_batch_invariant_mode():
         assert torch.equal(torch.mm(a, b), a @ b)
         assert torch.softmax(a, -1).shape == (4, 5)
         assert a.mean(-1).shape == (4,)
+        assert torch.nn.functional.conv1d(torch.ones(1, 2, 5), torch.ones(3, 2, 2)).shape == (1, 3, 4)
     names = [op for op, _ in bio.batch_invariant_ops._OVERRIDES]
     assert names == [
-        "aten::mm", "aten::addmm", "aten::linear", "aten::bmm", "aten::scaled_dot_product_attention",
-        "aten::_softmax", "aten::_log_softmax", "aten::mean.dim", "aten::linalg_vector_norm",
+        "aten::mm", "aten::addmm", "aten::linear", "aten::bmm", "aten::convolution",
+        "aten::scaled_dot_product_attention", "aten::_softmax", "aten::_log_softmax", "aten::mean.dim",
+        "aten::linalg_vector_norm",
     ]
     assert bio.batch_invariant_ops._DISPATCH_KEY == "CUDA"
 

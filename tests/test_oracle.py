@@ -250,3 +250,101 @@ def test_moe_edge_shapes():
     assert oracle.moe(hidden[:0], torch.zeros(0, 1), torch.zeros(0, 1, dtype=torch.long), gate, gate, down).shape == (0, 4)
     z = oracle.moe(hidden, torch.zeros(3, 0), torch.zeros(3, 0, dtype=torch.long), gate, gate, down)
     assert z.shape == (3, 4) and torch.count_nonzero(z) == 0
+
+
+# ----------------------------------------------------------------------- convolution ----
+def _conv_loop(x, w, stride, padding, dilation, groups):
+    """Regular N-d convolution straight from its definition (python loops, float64)."""
+    nd = x.ndim - 2
+    B, C = x.shape[:2]
+    O, Cg = w.shape[:2]
+    k = w.shape[2:]
+    out_size = [(x.shape[2 + i] + 2 * padding[i] - dilation[i] * (k[i] - 1) - 1) // stride[i] + 1 for i in range(nd)]
+    out = torch.zeros(B, O, *out_size, dtype=torch.float64)
+    Og = O // groups
+    for b in range(B):
+        for o in range(O):
+            g = o // Og
+            for pos in np.ndindex(*out_size):
+                acc = 0.0
+                for c in range(Cg):
+                    for tap in np.ndindex(*k):
+                        src = [pos[i] * stride[i] - padding[i] + tap[i] * dilation[i] for i in range(nd)]
+                        if all(0 <= src[i] < x.shape[2 + i] for i in range(nd)):
+                            acc += float(x[(b, g * Cg + c, *src)]) * float(w[(o, c, *tap)])
+                out[(b, o, *pos)] = acc
+    return out
+
+
+def _conv_transpose_loop(x, w, groups):
+    """Non-overlapping transposed convolution (stride == kernel) from its definition."""
+    nd = x.ndim - 2
+    B, C = x.shape[:2]
+    Og = w.shape[1]
+    k = w.shape[2:]
+    Cg = C // groups
+    out = torch.zeros(B, Og * groups, *[x.shape[2 + i] * k[i] for i in range(nd)], dtype=torch.float64)
+    for b in range(B):
+        for c in range(C):
+            g = c // Cg
+            for pos in np.ndindex(*x.shape[2:]):
+                for o in range(Og):
+                    for tap in np.ndindex(*k):
+                        dst = [pos[i] * k[i] + tap[i] for i in range(nd)]
+                        out[(b, g * Og + o, *dst)] += float(x[(b, c, *pos)]) * float(w[(c, o, *tap)])
+    return out
+
+
+@pytest.mark.parametrize(("xs", "ws", "stride", "padding", "dilation", "groups"), (
+    ((2, 4, 9), (6, 2, 3), (2,), (3,), (2,), 2),
+    ((2, 4, 6, 5), (6, 2, 3, 2), (2, 1), (1, 0), (2, 1), 2),
+    ((1, 3, 4, 5, 4), (2, 3, 2, 3, 2), (1, 2, 1), (1, 0, 1), (1, 1, 2), 1),
+    ((2, 4, 7), (4, 1, 3), (1,), (1,), (1,), 4),  # depthwise 1-D
+))
+def test_conv_integer_valued_matches_definition(xs, ws, stride, padding, dilation, groups):
+    """Integer operands: every sum is exact in float64 and bf16-representable (|sum| < 256), so
+    the oracle must reproduce the loop bit for bit, bias included."""
+    x = ints(*xs, lo=-3, hi=3, seed=9100).to(BF16)
+    w = ints(*ws, lo=-2, hi=2, seed=9101).to(BF16)
+    bias = ints(ws[0], lo=-4, hi=4, seed=9102).to(BF16)
+    loop = _conv_loop(x.double(), w.double(), stride, padding, dilation, groups)
+    assert loop.abs().max() < 200
+    out = oracle.conv(x, w, bias, stride, padding, dilation, False, (0,) * len(stride), groups)
+    assert torch.equal(out.double(), loop + bias.double().reshape(1, -1, *([1] * len(stride))))
+
+
+@pytest.mark.parametrize(("xs", "ws", "groups"), (((2, 4, 2, 3), (4, 3, 2, 2), 2), ((1, 2, 2, 1, 2), (2, 2, 3, 1, 2), 1)))
+def test_conv_transpose_integer_valued_matches_definition(xs, ws, groups):
+    x = ints(*xs, lo=-3, hi=3, seed=9110).to(BF16)
+    w = ints(*ws, lo=-2, hi=2, seed=9111).to(BF16)
+    nd = len(xs) - 2
+    k = tuple(ws[2:])
+    bias = ints(ws[1] * groups, lo=-4, hi=4, seed=9112).to(BF16)
+    loop = _conv_transpose_loop(x.double(), w.double(), groups)
+    out = oracle.conv(x, w, bias, k, (0,) * nd, (1,) * nd, True, (0,) * nd, groups)
+    assert torch.equal(out.double(), loop + bias.double().reshape(1, -1, *([1] * nd)))
+
+
+def test_conv_bias_rounding_follows_the_path():
+    """Depthwise 1-D rounds once after the bias; every other form rounds the dot product and then
+    the sum with the bias.  With dot = 1 + 2^-8 and bias = 2^-8 (bf16): one rounding gives
+    1 + 2^-7, two give round(1 + 2^-8) = 1 (tie to even), then 1 + 2^-8 -> 1."""
+    x = torch.tensor([[[1.0, 2.0**-8]]]).to(BF16)  # one channel, two taps
+    w = torch.tensor([[[1.0, 1.0]]]).to(BF16)
+    b = torch.tensor([2.0**-8]).to(BF16)
+    depthwise = oracle.conv(x, w, b, (1,), (0,), (1,), False, (0,), 1)  # groups == C == O == 1
+    assert depthwise.item() == 1 + 2.0**-7
+    x2 = x.expand(1, 2, 2).contiguous()
+    w2 = torch.tensor([[[1.0, 1.0], [0.0, 0.0]]]).to(BF16)  # one output over two channels
+    regular = oracle.conv(x2, w2, b, (1,), (0,), (1,), False, (0,), 1)
+    assert regular.item() == 1.0
+
+
+def test_conv_delta_kernel_copies_and_shifts():
+    x = torch.randn(2, 3, 6, 7, generator=torch.Generator().manual_seed(9120))
+    w = torch.zeros(3, 1, 3, 3)
+    w[:, 0, 2, 0] = 1.0  # tap (2, 0) of every channel
+    out = oracle.conv(x, w, None, (1, 1), (1, 1), (1, 1), False, (0, 0), 3)
+    # output (h, w) reads input (h + 1, w - 1)
+    assert torch.equal(out[:, :, :5, 1:], x[:, :, 1:, :6])
+    assert torch.count_nonzero(out[:, :, 5, :]) == 0 and torch.count_nonzero(out[:, :, :, 0]) == 0
