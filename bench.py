@@ -16,6 +16,7 @@ every kernel family) and writes them to REPORT.json; the headline line is unchan
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import math
 import os
@@ -54,11 +55,29 @@ def profile_kernel(which, iters):
     iters times: the programs the FETCH_SIZE / WRITE_SIZE counter runs observe."""
     import torch
 
+    import batch_invariant_ops as bio
+
     if which == "copy":
         src = torch.ones(512 * 2**20 // 4, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(iters):
             dst.copy_(src)
+    elif which == "sdpa":
+        # configs[2] causal at B = 16 (fused attention kernel)
+        g = torch.Generator().manual_seed(3)
+        q = torch.randn(16, 16, 1024, 128, generator=g).to(torch.bfloat16).cuda()
+        k = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).cuda()
+        for _ in range(iters):
+            bio.scaled_dot_product_attention_batch_invariant(q, k, v, is_causal=True, enable_gqa=True)
+    elif which == "softmax":
+        x = torch.randn(16 * 16 * 1024, 1024, device="cuda").to(torch.bfloat16)
+        for _ in range(iters):
+            bio.softmax(x, -1)
+    elif which == "norm":
+        x = torch.randn(65536, 2048, device="cuda").to(torch.bfloat16)
+        for _ in range(iters):
+            bio.linalg_vector_norm_batch_invariant(x, dim=-1)
     else:
         from batch_invariant_ops import linear_batch_invariant
 
@@ -83,10 +102,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "copy"),
+        choices=("gemm", "copy", "sdpa", "softmax", "norm"),
         default=None,
-        help="only launch the roofline kernel (gemm) or a 512 MiB device copy (copy) --iters "
-        "times, for hardware-counter runs; prints no JSON line",
+        help="only launch the roofline kernel (gemm), a 512 MiB device copy (copy), configs[2] "
+        "causal attention at B=16 (sdpa), a 262144x1024 bf16 softmax (softmax) or a 65536x2048 "
+        "bf16 row L2 norm (norm) --iters times, for counter runs; prints no JSON line",
     )
     p.add_argument("--iters", type=int, default=10)
     return p.parse_args()
@@ -148,6 +168,20 @@ def _bitwise(a, b):
     import torch
 
     return bool(torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)))
+
+
+@contextlib.contextmanager
+def _materialized_attention():
+    """Select the materialised-score attention path (for comparison timings)."""
+    old = os.environ.get("BIOPS_ATTENTION_MATERIALIZE")
+    os.environ["BIOPS_ATTENTION_MATERIALIZE"] = "1"
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ["BIOPS_ATTENTION_MATERIALIZE"]
+        else:
+            os.environ["BIOPS_ATTENTION_MATERIALIZE"] = old
 
 
 def run_all():
@@ -243,8 +277,14 @@ def run_all():
         o16 = run(16)
         c3[f"{name}_bitwise_B1_B4_B16"] = _bitwise(run(1), o16[:1]) and _bitwise(run(4), o16[:4])
         ms = event_time(lambda: run(16), 5)
+        # useful work: QK^T and PV over the visible (query, key) pairs
+        pairs = 1024 * 1025 / 2 if name == "causal" else 1024 * 1024
         c3[f"{name}_B16_ms"] = ms
-        c3[f"{name}_B16_tflops_executed"] = 4 * 16 * 16 * 1024 * 1024 * 128 / (ms * 1e-3) / 1e12
+        c3[f"{name}_B16_tflops_useful"] = 4 * 16 * 16 * pairs * 128 / (ms * 1e-3) / 1e12
+        with _materialized_attention():
+            ms_m = event_time(lambda: run(16), 5)
+            c3[f"{name}_B16_materialized_ms"] = ms_m
+            c3[f"{name}_bitwise_materialized_B1_B16"] = _bitwise(run(1), run(16)[:1])
     report["C3_sdpa"] = c3
     del q, k, v, mask
 
@@ -266,13 +306,19 @@ def run_all():
         alone = bio.varlen_scaled_dot_product_attention_batch_invariant(
             q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], one, one, is_causal=True, causal_type="BottomRight")
         bi &= _bitwise(alone, out[:, s0:s1])
-    ms = event_time(lambda: bio.varlen_scaled_dot_product_attention_batch_invariant(
-        q, k, v, cu_d, cu_d, is_causal=True, causal_type="BottomRight"), 5)
-    sumsq = float((lengths.double() ** 2).sum())
+    def run_varlen():
+        return bio.varlen_scaled_dot_product_attention_batch_invariant(
+            q, k, v, cu_d, cu_d, is_causal=True, causal_type="BottomRight")
+
+    ms = event_time(run_varlen, 5)
+    with _materialized_attention():
+        ms_m = event_time(run_varlen, 5)
+    pairs = float((lengths.double() * (lengths.double() + 1) / 2).sum())
     report["C4_varlen"] = {
         "bitwise_seq_alone_vs_packed": bi,
         "ms": ms,
-        "tflops_executed": 4 * 8 * 64 * sumsq / (ms * 1e-3) / 1e12,
+        "tflops_useful": 4 * 8 * 64 * pairs / (ms * 1e-3) / 1e12,
+        "materialized_ms": ms_m,
         "total_tokens": total,
     }
     del q, k, v

@@ -161,6 +161,38 @@ int biops_conv(int dtype, int nd, int transposed, int64_t batch, int64_t cin, co
 
 /* ------------------------------------------------------------------- attention ---- */
 
+/* 1 when biops_sdpa_fused / biops_varlen_sdpa_fused take this dtype and head sizes: bf16 or
+ * fp16, 1 <= d, dv <= 128, both multiples of 8; 0 otherwise.  No reference counterpart (the
+ * reference has one eager path); callers pick the fused or the materialised entry with it. */
+int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv);
+
+/* Same operator and arguments as biops_sdpa, without a score matrix in memory and without a
+ * workspace: each 128-row query tile walks 64-key blocks in order twice (row max and sum, then
+ * P V), with the roundings of the eager composite (S, S*scale, S+mask and the normalised P
+ * rounded to dtype).  S is bitwise the materialised S; the row sum may differ from the row
+ * kernel's in the last fp32 bits.  Needs biops_attention_fused_supported, 16-byte aligned q/k/v
+ * and strides that are multiples of 8 elements (BIOPS_ERR_LAYOUT otherwise).
+ * Replaces scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1148-1213). */
+int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+                     int64_t d, int64_t dv,
+                     const void* q, int64_t sqB, int64_t sqH, int64_t sqL,
+                     const void* k, int64_t skB, int64_t skH, int64_t skL,
+                     const void* v, int64_t svB, int64_t svH, int64_t svL,
+                     const void* mask, int mask_dtype, int64_t mB, int64_t mH, int64_t mI, int64_t mJ,
+                     int causal, float scale, void* out, void* stream);
+
+/* Packed varlen attention with the fused kernel: same arguments as biops_varlen_sdpa without
+ * the workspace (the plan from biops_varlen_plan, dv <= 128).  out rows outside every
+ * sequence are not written.  Same layout conditions as biops_sdpa_fused.
+ * Replaces varlen_scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1216-1344). */
+int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
+                            const void* q, int64_t sq_t, int64_t sq_h,
+                            const void* k, int64_t sk_t, int64_t sk_h,
+                            const void* v, int64_t sv_t, int64_t sv_h,
+                            void* out, int64_t so_t, int64_t so_h,
+                            const int64_t* dplan, const int64_t* hplan, int causal, float scale,
+                            void* stream);
+
 /* Workspace bytes biops_sdpa needs (the materialised score/probability matrices). */
 int64_t biops_sdpa_workspace_size(int dtype, int64_t batch, int64_t hq, int64_t lq, int64_t lk);
 

@@ -444,6 +444,20 @@ def linalg_vector_norm_batch_invariant(
 
 
 # -------------------------------------------------------------------- attention ----
+def _fused_attention_ok(dtype, d, dv, *tensors):
+    """True when the fused attention kernel takes this call: bf16/fp16, head sizes <= 128 and
+    multiples of 8, 16-byte aligned rows.  ``BIOPS_ATTENTION_MATERIALIZE=1`` selects the
+    materialised-score path (same operator, row sums in the row kernel's order)."""
+    if dtype not in (torch.bfloat16, torch.float16) or nat.env_flag("BIOPS_ATTENTION_MATERIALIZE", False):
+        return False
+    if not nat.load().biops_attention_fused_supported(nat.dtype_code(dtype), d, dv):
+        return False
+    for t in tensors:
+        if t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:-1]):
+            return False
+    return True
+
+
 def _sdpa_glue(q4, k4, v4, group, mask4, scale, out_dtype):
     """Eager SDPA for mask dtypes the fused softmax does not take (type promotion): the GEMMs
     and the softmax are the library kernels, the masking is the reference's elementwise glue
@@ -537,6 +551,19 @@ def scaled_dot_product_attention_batch_invariant(
     out = torch.empty((B, Hq, Lq, Dv), dtype=query.dtype, device=query.device)
     if out.numel() == 0:
         return out.reshape(*leading, Lq, Dv)
+    causal_code = nat.CAUSAL_TOP_LEFT if is_causal else nat.CAUSAL_NONE
+    if _fused_attention_ok(query.dtype, D, Dv, q4, k4, v4):
+        nat.call(
+            "biops_sdpa_fused",
+            nat.dtype_code(query.dtype), B, Hq, Hkv, Lq, Lk, D, Dv,
+            q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2),
+            k4.data_ptr(), k4.stride(0), k4.stride(1), k4.stride(2),
+            v4.data_ptr(), v4.stride(0), v4.stride(1), v4.stride(2),
+            mask4.data_ptr() if mask4 is not None else None, mask_code,
+            *(mask4.stride() if mask4 is not None else (0, 0, 0, 0)),
+            causal_code, float(scale_value), out.data_ptr(), nat.stream_of(out),
+        )
+        return out.reshape(*leading, Lq, Dv)
     ws_bytes = nat.load().biops_sdpa_workspace_size(nat.dtype_code(query.dtype), B, Hq, Lq, Lk)
     workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=query.device)
     nat.call(
@@ -547,7 +574,7 @@ def scaled_dot_product_attention_batch_invariant(
         v4.data_ptr(), v4.stride(0), v4.stride(1), v4.stride(2),
         mask4.data_ptr() if mask4 is not None else None, mask_code,
         *(mask4.stride() if mask4 is not None else (0, 0, 0, 0)),
-        nat.CAUSAL_TOP_LEFT if is_causal else nat.CAUSAL_NONE, float(scale_value),
+        causal_code, float(scale_value),
         out.data_ptr(), workspace.data_ptr(), workspace.numel(),
         nat.stream_of(out),
     )
@@ -645,12 +672,24 @@ def varlen_scaled_dot_product_attention_batch_invariant(
 
     q, k, v = tokens_heads(query), tokens_heads(key), tokens_heads(value)
     dplan = torch.from_numpy(plan).to(query.device)
-    workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
     if is_causal:
         causal = nat.CAUSAL_BOTTOM_RIGHT if causal_name == "BottomRight" else nat.CAUSAL_TOP_LEFT
     else:
         causal = nat.CAUSAL_NONE
     scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
+    if _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v):
+        nat.call(
+            "biops_varlen_sdpa_fused",
+            nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
+            q.data_ptr(), q.stride(1), q.stride(2),
+            k.data_ptr(), k.stride(1), k.stride(2),
+            v.data_ptr(), v.stride(1), v.stride(2),
+            output.data_ptr(), output.stride(1), output.stride(2),
+            dplan.data_ptr(), plan.ctypes.data, causal, float(scale_value),
+            nat.stream_of(output),
+        )
+        return output
+    workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
     nat.call(
         "biops_varlen_sdpa",
         nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,

@@ -1,0 +1,580 @@
+// Fused attention for 16-bit inputs: no score matrix in memory.
+//
+// One workgroup (four wavefronts) owns a tile of 128 query rows of one (batch, head) -- or of
+// one (sequence, head) of a packed varlen batch -- and walks the key/value rows in fixed blocks
+// of 64, in order, twice:
+//   pass 1: S = Q K^T for the block, the reference's transform (below), then the running row
+//           maximum m and the row sum l of exp(s - m) (rescaled when m grows);
+//   pass 2: S again, P = round(exp(s - m) * (1 / l)), O += P V.
+// The transform and the roundings are the eager composite's (batch_invariant_ops.py:1194-1212):
+//   s = round(round(S) * scale); causal / boolean mask -> -inf; additive mask -> round(s + mask);
+// P is normalised and rounded to the input dtype before it meets V; a row with no visible key
+// gives zeros.  S itself is produced by the same MFMA sequence as the GEMM path (128-byte steps
+// of the head dimension, chunk pairs in order), so its bits equal the materialised S.  The row
+// sum is accumulated per lane in block order and combined across the two half-wavefronts, so it
+// may differ from the row kernel's sum in the last fp32 bits.
+//
+// Batch invariance: a tile's arithmetic depends only on its own sequence (query rows, keys,
+// values, mask) and on the head dimension; the block order and the MFMA sequence are fixed.
+//
+// Register layout (wavefront w owns query rows 32w .. 32w+31 of the tile).  The scores are
+// computed transposed, S^T = K Q^T, with K as the MFMA A operand and Q as B, so that lane L holds
+// query row L % 32 and keys 8j + 4(L/32) + i (j, i = 0..3) of each 32-key block.  Those eight
+// keys per 16-key chunk are exactly one A-operand fragment of the P V product (with the key order
+// inside the chunk permuted the same way for P and for V), so P goes from the accumulators to
+// the next MFMA without passing through LDS.  V fragments come from LDS with the transposing
+// 64-bit read.
+#include "gemm.h"
+#include "rowops.h"
+
+namespace biops {
+
+struct FusedArgs {
+  const void* q; const void* k; const void* v; void* out;
+  const void* mask;
+  const int64_t* plan;  // varlen work list (VARLEN kernels)
+  int64_t hq, group, hkv, lq, lk, d, dv;
+  // element strides: batch (unused for varlen), head, row (token)
+  int64_t sqB, sqH, sqL, skB, skH, skL, svB, svH, svL, soB, soH, soL;
+  int64_t mB, mH, mI, mJ;
+  int64_t items, tiles;
+  float scale;
+  int causal;
+};
+
+constexpr int kFusedBM = 128;  // query rows per workgroup
+constexpr int kFusedBN = 64;   // keys per block
+
+template <typename T, int DP, int DVP>
+struct FusedTile {
+  static constexpr int THREADS = 256;
+  static constexpr int KCH = DP / 8;   // 16-byte chunks per K row
+  static constexpr int VCH = DVP / 8;  // 16-byte chunks per V row
+  static constexpr int K_BYTES = kFusedBN * DP * 2;
+  static constexpr int V_BYTES = kFusedBN * DVP * 2;
+  static constexpr int LDS_BYTES = 2 * (K_BYTES + V_BYTES);
+  static constexpr int K_LOADS = kFusedBN * KCH / THREADS;
+  static constexpr int V_LOADS = kFusedBN * VCH / THREADS;
+  static constexpr int QF = DP / 16;   // MFMAs per 32x32 score block
+  static constexpr int OF = DVP / 32;  // 32-column output blocks
+  static_assert(K_LOADS >= 1 && V_LOADS >= 1, "block loads");
+
+  // K rows: 16-byte chunk c of row r at slot c ^ swz(r); 16 consecutive rows reading the same
+  // chunk hit 16 distinct 16-byte bank slots.
+  __device__ static __forceinline__ int k_off(int r, int c) {
+    if constexpr (KCH == 16) return r * (DP * 2) + ((c ^ (r & 15)) << 4);
+    else return r * (DP * 2) + ((c ^ ((r >> 1) & 7)) << 4);
+  }
+  // V rows: the layout of the GEMM's N-major operand stage (transposing reads, 4 rows at once).
+  __device__ static __forceinline__ int v_off(int r, int col) { return lds_off_n<VCH>(r, col); }
+};
+
+// Per-tile geometry, decoded from the tile index.
+struct FusedGeom {
+  const char* q;  // first query row of the tile, this head
+  const char* k;  // first key row of the sequence, this kv head
+  const char* v;
+  char* out;      // first output row of the tile, this head
+  int64_t b, h;   // batch (0 for varlen) and query head
+  int64_t qrows;  // valid query rows in the tile
+  int64_t i0;     // index of the tile's first row inside its sequence
+  int64_t ql, kl; // sequence lengths
+};
+
+template <typename T, bool VARLEN>
+__device__ __forceinline__ bool fused_geom(const FusedArgs& a, int64_t t, FusedGeom& g) {
+  constexpr int E = sizeof(T);
+  int64_t h, qt, qstart = 0, kstart = 0, b = 0;
+  if constexpr (VARLEN) {
+    // item whose first tile (plan word 6) is the last one <= t
+    int64_t lo = 0, hi = a.items - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) >> 1;
+      if (a.plan[kPlanHeader + kPlanStride * mid + 6] <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t* p = a.plan + kPlanHeader + kPlanStride * lo;
+    g.ql = p[1];
+    g.kl = p[3];
+    qstart = p[0];
+    kstart = p[2];
+    const int64_t local = t - p[6];
+    const int64_t qtiles = cdiv(g.ql, kFusedBM);
+    if (local < 0 || local >= qtiles * a.hq) return false;
+    qt = qtiles - 1 - local / a.hq;  // longest key ranges first (causal)
+    h = local % a.hq;
+  } else {
+    g.ql = a.lq;
+    g.kl = a.lk;
+    const int64_t qtiles = cdiv(a.lq, kFusedBM);
+    // heads sharing a key/value head are adjacent; longest key ranges first within a head
+    const int64_t gi = t % a.group;
+    int64_t rest = t / a.group;
+    qt = qtiles - 1 - rest % qtiles;
+    rest /= qtiles;
+    const int64_t hk = rest % a.hkv;
+    b = rest / a.hkv;
+    h = hk * a.group + gi;
+  }
+  const int64_t hk = h / a.group;
+  g.i0 = qt * kFusedBM;
+  g.qrows = g.ql - g.i0 < kFusedBM ? g.ql - g.i0 : kFusedBM;
+  g.q = reinterpret_cast<const char*>(a.q) + E * (b * a.sqB + h * a.sqH + (qstart + g.i0) * a.sqL);
+  g.k = reinterpret_cast<const char*>(a.k) + E * (b * a.skB + hk * a.skH + kstart * a.skL);
+  g.v = reinterpret_cast<const char*>(a.v) + E * (b * a.svB + hk * a.svH + kstart * a.svL);
+  g.out = reinterpret_cast<char*>(a.out) + E * (b * a.soB + h * a.soH + (qstart + g.i0) * a.soL);
+  g.b = b;
+  g.h = h;
+  return true;
+}
+
+// Round two fp32 values to T (and back to fp32) -- one paired conversion for bf16.
+template <typename T>
+__device__ __forceinline__ void round2(float& x0, float& x1) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t pk = f32x2_to_bf16x2_bits(x0, x1);
+    x0 = __uint_as_float(pk << 16);
+    x1 = __uint_as_float(pk & 0xffff0000u);
+  } else {
+    x0 = Num<T>::round(x0);
+    x1 = Num<T>::round(x1);
+  }
+}
+
+// First MFMA of a chain: the accumulator input is the constant zero.
+template <typename T>
+__device__ __forceinline__ f32x16_t mfma_first(const u32x4_t& a, const u32x4_t& b) {
+  const f32x16_t z = {};
+  if constexpr (std::is_same<T, bf16_t>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), z, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), z, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  if constexpr (std::is_same<T, bf16_t>::value) return f32x2_to_bf16x2_bits(x, y);
+  else return (uint32_t)Num<T>::to_bits(x) | ((uint32_t)Num<T>::to_bits(y) << 16);
+}
+
+// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD
+// without a mask; the masked kernels keep the mask values of a block in registers as well and
+// run one wavefront per SIMD with the full register file.
+template <typename T, int DP, int DVP, int MASK, bool VARLEN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASK ? 1 : 2, 2)))
+void fused_attn_kernel(FusedArgs a) {
+  using F = FusedTile<T, DP, DVP>;
+  __shared__ __attribute__((aligned(16))) char smem[F::LDS_BYTES];
+  const int64_t t = xcd_slot(blockIdx.x, gridDim.x);
+  if (t >= a.tiles) return;
+  FusedGeom g;
+  if (!fused_geom<T, VARLEN>(a, t, g)) return;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  constexpr int E = sizeof(T);
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+  const int ql = (int)g.ql, kl = (int)g.kl, qrows = (int)g.qrows, i0 = (int)g.i0;
+  const int shift = a.causal == BIOPS_CAUSAL_BOTTOM_RIGHT ? kl - ql : 0;
+
+  // Key limit of tile-local row r: keys n >= lim(r) are masked out (sequence end, causal
+  // alignment).  Limits grow with the row.
+  auto row_lim = [&](int r) -> int {
+    if (a.causal == BIOPS_CAUSAL_NONE) return kl;
+    const int c = i0 + r + shift + 1;
+    return c < 0 ? 0 : (c > kl ? kl : c);
+  };
+  // Query row of this lane (column of S^T); rows past the tile's end see no key.
+  const int rloc = 32 * w + l32;
+  const bool row_ok = rloc < qrows;
+  const int lim = row_ok ? row_lim(rloc) : 0;
+  const int tile_lim = qrows > 0 ? row_lim(qrows - 1) : 0;
+  const int wrows = qrows - 32 * w;
+  // keys this wavefront needs (wave-uniform), and key blocks of the workgroup
+  const int wave_lim = wrows > 0 ? row_lim(32 * w + (wrows < 32 ? wrows : 32) - 1) : 0;
+  const int nblk = (tile_lim + kFusedBN - 1) / kFusedBN;
+
+  const char* mrow = nullptr;
+  if constexpr (MASK != 0) {
+    if (row_ok) {
+      constexpr int ME = MASK == 1 ? 1 : E;  // mask strides count mask elements
+      mrow = reinterpret_cast<const char*>(a.mask) + ME * (g.b * a.mB + g.h * a.mH + (int64_t)(i0 + rloc) * a.mI);
+    }
+  }
+
+  // Q fragments (B operand of S^T = K Q^T): lane holds row l32, head-dim chunk 2cc + hf.
+  u32x4_t qf[F::QF];
+#pragma unroll
+  for (int cc = 0; cc < F::QF; ++cc) {
+    const int d0 = 16 * cc + 8 * hf;
+    qf[cc] = (row_ok && d0 < a.d) ? *reinterpret_cast<const u32x4_t*>(g.q + E * (rloc * a.sqL + d0)) : zero4;
+  }
+
+  char* const kbuf0 = smem;
+  char* const vbuf0 = smem + 2 * F::K_BYTES;
+
+  // Block loads through registers: thread chunk s = tid + 256p is row s / CH, chunk s % CH.
+  // Each thread keeps the byte offset of its chunks inside a block (head-dim chunks past the
+  // problem point at chunk 0) and a validity flag.
+  uint32_t koff[F::K_LOADS], voff[F::V_LOADS];
+  bool kdv[F::K_LOADS], vdv[F::V_LOADS];
+  int krow[F::K_LOADS], vrow_[F::V_LOADS];
+#pragma unroll
+  for (int p = 0; p < F::K_LOADS; ++p) {
+    const int s = tid + F::THREADS * p;
+    krow[p] = s / F::KCH;
+    const int c = s % F::KCH;
+    kdv[p] = 8 * c < a.d;
+    koff[p] = (uint32_t)(E * (krow[p] * a.skL + (kdv[p] ? 8 * c : 0)));
+  }
+#pragma unroll
+  for (int p = 0; p < F::V_LOADS; ++p) {
+    const int s = tid + F::THREADS * p;
+    vrow_[p] = s / F::VCH;
+    const int c = s % F::VCH;
+    vdv[p] = 8 * c < a.dv;
+    voff[p] = (uint32_t)(E * (vrow_[p] * a.svL + (vdv[p] ? 8 * c : 0)));
+  }
+  u32x4_t kr[F::K_LOADS];
+  u32x4_t vr[F::V_LOADS];
+  // Rows of block blk: a whole block with the full head dimension reads in place; otherwise
+  // rows n >= kl and chunks past the head dimension are zeros (read from a valid address).
+  const bool kfull = a.d == DP, vfull = a.dv == DVP;
+  auto load_k = [&](int blk) {
+    const int n0 = blk * kFusedBN;
+    const char* base = g.k + (int64_t)E * n0 * a.skL;
+    if (n0 + kFusedBN <= kl && kfull) {
+#pragma unroll
+      for (int p = 0; p < F::K_LOADS; ++p) kr[p] = *reinterpret_cast<const u32x4_t*>(base + koff[p]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < F::K_LOADS; ++p) {
+        const bool in = n0 + krow[p] < kl;
+        const int64_t off = in ? (int64_t)koff[p] : -(int64_t)E * n0 * a.skL;  // row 0 of the sequence
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(base + off);
+        kr[p] = (kdv[p] && in) ? x : zero4;
+      }
+    }
+  };
+  auto store_k = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < F::K_LOADS; ++p) {
+      const int s = tid + F::THREADS * p;
+      *reinterpret_cast<u32x4_t*>(kbuf0 + buf * F::K_BYTES + F::k_off(s / F::KCH, s % F::KCH)) = kr[p];
+    }
+  };
+  auto load_v = [&](int blk) {
+    const int n0 = blk * kFusedBN;
+    const char* base = g.v + (int64_t)E * n0 * a.svL;
+    if (n0 + kFusedBN <= kl && vfull) {
+#pragma unroll
+      for (int p = 0; p < F::V_LOADS; ++p) vr[p] = *reinterpret_cast<const u32x4_t*>(base + voff[p]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < F::V_LOADS; ++p) {
+        const bool in = n0 + vrow_[p] < kl;
+        const int64_t off = in ? (int64_t)voff[p] : -(int64_t)E * n0 * a.svL;
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(base + off);
+        vr[p] = (vdv[p] && in) ? x : zero4;
+      }
+    }
+  };
+  auto store_v = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < F::V_LOADS; ++p) {
+      const int s = tid + F::THREADS * p;
+      *reinterpret_cast<u32x4_t*>(vbuf0 + buf * F::V_BYTES + F::v_off(s / F::VCH, 8 * (s % F::VCH))) = vr[p];
+    }
+  };
+
+  // Smallest key limit among the wavefront's rows: key half-blocks below it need no limit test.
+  const int wave_min_lim = wrows > 0 ? row_lim(32 * w) : 0;
+  // Mask rows read 4 consecutive keys at once when they are contiguous and aligned.
+  const bool mvec = MASK != 0 && a.mJ == 1 && ((reinterpret_cast<uintptr_t>(a.mask) & 7) == 0) &&
+                    ((a.mB | a.mH | a.mI) & 3) == 0;
+
+  // Transformed scores of keys 32 hb .. 32 hb + 31 of block blk: sc[r] is key
+  // 64 blk + 32 hb + 8(r/4) + 4 hf + r%4 of this lane's row.
+  f32x16_t sc;
+  auto scores = [&](int buf, int blk, int hb) {
+    const int nb = blk * kFusedBN + 32 * hb + 4 * hf;
+    // mask values of the 16 keys, fetched before the MFMAs
+    float mv[16];
+    if constexpr (MASK != 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n0 = nb + 8 * j;
+        if (mvec && n0 + 3 < lim) {
+          if constexpr (MASK == 1) {
+            const uint32_t x = *reinterpret_cast<const uint32_t*>(mrow + n0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mv[4 * j + e] = ((x >> (8 * e)) & 0xffu) ? 0.f : -INFINITY;
+          } else {
+            const u32x2_t x = *reinterpret_cast<const u32x2_t*>(mrow + E * n0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mv[4 * j + e] = Num<T>::from_bits((x[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int n = n0 + e;
+            if (n < lim) {
+              if constexpr (MASK == 1) mv[4 * j + e] = reinterpret_cast<const uint8_t*>(mrow)[(int64_t)n * a.mJ] ? 0.f : -INFINITY;
+              else mv[4 * j + e] = Num<T>::load(reinterpret_cast<const T*>(mrow) + (int64_t)n * a.mJ);
+            } else {
+              mv[4 * j + e] = 0.f;
+            }
+          }
+        }
+      }
+    }
+    const char* kb = kbuf0 + buf * F::K_BYTES;
+    {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, hf));
+      sc = mfma_first<T>(kf, qf[0]);
+    }
+#pragma unroll
+    for (int cc = 1; cc < F::QF; ++cc) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf));
+      Mfma<T>::step(sc, kf, qf[cc]);
+    }
+    // Keys 8(r/4) + r%4 (relative to nb) at or past rel = lim - nb are masked out; when every
+    // key of the half-block is visible to every row of the wavefront the test is skipped.
+    const int rel = lim - nb;
+    auto transform = [&](auto all_visible) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float s0 = sc[r], s1 = sc[r + 1];
+        round2<T>(s0, s1);
+        s0 *= a.scale;
+        s1 *= a.scale;
+        round2<T>(s0, s1);
+        if constexpr (!decltype(all_visible)::value) {
+          const int o = 8 * (r >> 2) + (r & 3);
+          s0 = o < rel ? s0 : -INFINITY;
+          s1 = o + 1 < rel ? s1 : -INFINITY;
+        }
+        if constexpr (MASK == 1) {
+          s0 += mv[r];  // 0 (keep) or -inf
+          s1 += mv[r + 1];
+        } else if constexpr (MASK == 2) {
+          s0 += mv[r];
+          s1 += mv[r + 1];
+          round2<T>(s0, s1);
+        }
+        sc[r] = s0;
+        sc[r + 1] = s1;
+      }
+    };
+    if (blk * kFusedBN + 32 * hb + 32 <= wave_min_lim) transform(std::true_type{});
+    else transform(std::false_type{});
+  };
+
+  // ---------------------------------------------------------------- pass 1: m, l ----
+  // Running maximum m (shared by both half-wavefronts of a row) and this half's sum l of
+  // exp(s - m), rescaled when m grows; 32-key steps in order.
+  float m = -INFINITY, l = 0.f;
+  if (nblk > 0) {
+    load_k(0);
+    store_k(0);
+    __syncthreads();
+  }
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) load_k(blk + 1);
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      if (blk * kFusedBN + 32 * hb < wave_lim) {
+        scores(blk & 1, blk, hb);
+        float bm = sc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        // m = -inf until a visible key appears: the shift stays 0 and every term is exp(-inf) = 0
+        const float mn = fmaxf(m, bm);
+        const float sh = (mn == -INFINITY ? 0.f : mn) * kLog2e;
+        const float corr = __builtin_amdgcn_exp2f(m * kLog2e - sh);
+        float part = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kLog2e, -sh));
+        l = l * corr + part;
+        m = mn;
+      }
+    }
+    if (blk + 1 < nblk) store_k((blk + 1) & 1);
+    __syncthreads();
+  }
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const bool dead = (m == -INFINITY) || (lt == 0.f);
+  const float inv = dead ? 0.f : 1.0f / lt;
+  const float shl2e = (m == -INFINITY ? 0.f : m) * kLog2e;
+
+  // ---------------------------------------------------------------- pass 2: P V ----
+  f32x16_t oacc[F::OF];
+#pragma unroll
+  for (int e = 0; e < F::OF; ++e)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[e][r] = 0.f;
+  if (nblk > 0) {
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    store_v(0);
+    __syncthreads();
+  }
+  // V fragment source (transposing read): lane s of a 16-lane group points at row k0 + s/4,
+  // column n0 + 4(s%4), and receives rows k0..k0+3 of column n0 + s.
+  const int vrow = 4 * hf + ((lane & 15) >> 2);
+  const int vcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) {
+      load_k(blk + 1);
+      load_v(blk + 1);
+    }
+    const char* vb = vbuf0 + (blk & 1) * F::V_BYTES;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      if (blk * kFusedBN + 32 * hb < wave_lim) {
+        scores(blk & 1, blk, hb);
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          // 16-key chunk c = 2 hb + c2: this lane's keys 16c + 4hf + (0..3) and + 8
+          float p[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * c2 + e], kLog2e, -shl2e)) * inv;
+          const u32x4_t pa = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
+                              pack2<T>(p[6], p[7])};
+          const int row = 16 * (2 * hb + c2) + vrow;
+#pragma unroll
+          for (int e = 0; e < F::OF; ++e) {
+            const u32x2_t lo = lds_read_tr16(vb + F::v_off(row, 32 * e + vcol));
+            const u32x2_t hi = lds_read_tr16(vb + F::v_off(row + 8, 32 * e + vcol));
+            const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+            Mfma<T>::step(oacc[e], pa, vf);
+          }
+        }
+      }
+    }
+    if (blk + 1 < nblk) {
+      store_k((blk + 1) & 1);
+      store_v((blk + 1) & 1);
+    }
+    __syncthreads();
+  }
+
+  // O rows 32w + 8(r/4) + 4hf + r%4, column 32e + l32.
+#pragma unroll
+  for (int e = 0; e < F::OF; ++e) {
+    const int col = 32 * e + l32;
+    if (col >= a.dv) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int orow = 32 * w + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (orow < qrows) Num<T>::store(reinterpret_cast<T*>(g.out + E * (orow * a.soL)) + col, oacc[e][r]);
+    }
+  }
+}
+
+template <typename T, int DP, int DVP, int MASK, bool VARLEN>
+static int launch_fused_t(const FusedArgs& a, hipStream_t s) {
+  const int64_t grid = cdiv(a.tiles, 8) * 8;
+  if (grid > 0x7fffffffLL) return fail(BIOPS_ERR_SIZE, "too many attention tiles");
+  hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  return check_launch("fused_attn_kernel");
+}
+
+template <typename T, int MASK, bool VARLEN>
+static int launch_fused_d(const FusedArgs& a, hipStream_t s) {
+  if (a.d <= 64) {
+    if (a.dv <= 64) return launch_fused_t<T, 64, 64, MASK, VARLEN>(a, s);
+    return launch_fused_t<T, 64, 128, MASK, VARLEN>(a, s);
+  }
+  if (a.dv <= 64) return launch_fused_t<T, 128, 64, MASK, VARLEN>(a, s);
+  return launch_fused_t<T, 128, 128, MASK, VARLEN>(a, s);
+}
+
+template <int MASK, bool VARLEN>
+static int launch_fused(int dtype, const FusedArgs& a, hipStream_t s) {
+  if (dtype == BIOPS_F16) return launch_fused_d<f16_t, MASK, VARLEN>(a, s);
+  return launch_fused_d<bf16_t, MASK, VARLEN>(a, s);
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+static bool mult8(int64_t x) { return (x & 7) == 0; }
+// Byte offsets inside one key block (64 rows) are 32-bit.
+static bool block_fits(int64_t row_stride) { return row_stride >= 0 && 2 * kFusedBN * row_stride < (int64_t(1) << 31); }
+
+}  // namespace biops
+
+using namespace biops;
+
+extern "C" int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv) {
+  return (dtype == BIOPS_BF16 || dtype == BIOPS_F16) && d >= 1 && d <= 128 && dv >= 1 &&
+         dv <= 128 && mult8(d) && mult8(dv);
+}
+
+extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq,
+                                int64_t lk, int64_t d, int64_t dv, const void* q, int64_t sqB,
+                                int64_t sqH, int64_t sqL, const void* k, int64_t skB, int64_t skH,
+                                int64_t skL, const void* v, int64_t svB, int64_t svH, int64_t svL,
+                                const void* mask, int mask_dtype, int64_t mB, int64_t mH, int64_t mI,
+                                int64_t mJ, int causal, float scale, void* out, void* stream) {
+  if (!biops_attention_fused_supported(dtype, d, dv))
+    return fail(BIOPS_ERR_DTYPE, "fused attention takes bf16/fp16 with head dims <= 128, multiples of 8");
+  if (batch < 0 || hq < 0 || hkv <= 0 || lq < 0 || lk < 0) return fail(BIOPS_ERR_ARG, "invalid attention sizes");
+  if (hq % hkv != 0) return fail(BIOPS_ERR_ARG, "query heads must be a multiple of kv heads");
+  if (mask && causal != BIOPS_CAUSAL_NONE) return fail(BIOPS_ERR_ARG, "mask and causal are exclusive");
+  if (mask && mask_dtype != BIOPS_BOOL && mask_dtype != dtype)
+    return fail(BIOPS_ERR_DTYPE, "mask dtype must be bool or the score dtype");
+  if (batch == 0 || hq == 0 || lq == 0) return BIOPS_OK;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !mult8(sqB) || !mult8(sqH) || !mult8(sqL) ||
+      !mult8(skB) || !mult8(skH) || !mult8(skL) || !mult8(svB) || !mult8(svH) || !mult8(svL))
+    return fail(BIOPS_ERR_LAYOUT, "fused attention needs 16-byte aligned rows (strides multiples of 8)");
+  if (!block_fits(skL) || !block_fits(svL) || !block_fits(sqL) || lq >= (int64_t(1) << 31) || lk >= (int64_t(1) << 31))
+    return fail(BIOPS_ERR_LAYOUT, "fused attention row strides or lengths too large");
+  FusedArgs a{};
+  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = mask; a.plan = nullptr;
+  a.hq = hq; a.group = hq / hkv; a.hkv = hkv; a.lq = lq; a.lk = lk; a.d = d; a.dv = dv;
+  a.sqB = sqB; a.sqH = sqH; a.sqL = sqL; a.skB = skB; a.skH = skH; a.skL = skL;
+  a.svB = svB; a.svH = svH; a.svL = svL;
+  a.soB = hq * lq * dv; a.soH = lq * dv; a.soL = dv;
+  a.mB = mB; a.mH = mH; a.mI = mI; a.mJ = mJ;
+  a.tiles = batch * hq * cdiv(lq, kFusedBM);
+  a.scale = scale;
+  a.causal = causal;
+  hipStream_t s = (hipStream_t)stream;
+  if (!mask) return launch_fused<0, false>(dtype, a, s);
+  if (mask_dtype == BIOPS_BOOL) return launch_fused<1, false>(dtype, a, s);
+  return launch_fused<2, false>(dtype, a, s);
+}
+
+extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
+                                       const void* q, int64_t sq_t, int64_t sq_h, const void* k,
+                                       int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t,
+                                       int64_t sv_h, void* out, int64_t so_t, int64_t so_h,
+                                       const int64_t* dplan, const int64_t* hplan, int causal,
+                                       float scale, void* stream) {
+  if (!biops_attention_fused_supported(dtype, d, dv))
+    return fail(BIOPS_ERR_DTYPE, "fused attention takes bf16/fp16 with head dims <= 128, multiples of 8");
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(BIOPS_ERR_ARG, "invalid varlen head configuration");
+  if (!dplan || !hplan) return fail(BIOPS_ERR_ARG, "null plan");
+  const int64_t items = hplan[0];
+  if (items == 0) return BIOPS_OK;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !mult8(sq_t) || !mult8(sq_h) ||
+      !mult8(sk_t) || !mult8(sk_h) || !mult8(sv_t) || !mult8(sv_h))
+    return fail(BIOPS_ERR_LAYOUT, "fused attention needs 16-byte aligned rows (strides multiples of 8)");
+  if (!block_fits(sk_t) || !block_fits(sv_t) || !block_fits(sq_t))
+    return fail(BIOPS_ERR_LAYOUT, "fused attention row strides too large");
+  FusedArgs a{};
+  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = nullptr; a.plan = dplan;
+  a.hq = hq; a.group = hq / hkv; a.hkv = hkv; a.d = d; a.dv = dv;
+  a.sqL = sq_t; a.sqH = sq_h; a.skL = sk_t; a.skH = sk_h; a.svL = sv_t; a.svH = sv_h;
+  a.soL = so_t; a.soH = so_h;
+  a.items = items;
+  // With dv <= 128 the plan's PV tile count (one 128-row tile per head and query block) is the
+  // fused kernel's tile count, and word 6 of each item its first tile.
+  a.tiles = hplan[2];
+  a.scale = scale;
+  a.causal = causal;
+  return launch_fused<0, true>(dtype, a, (hipStream_t)stream);
+}
