@@ -158,8 +158,8 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
 }
 
 // MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD
-// without a mask; the masked kernels keep the mask values of a block in registers as well and
-// run one wavefront per SIMD with the full register file.
+// without a mask; the masked kernels (mask words of a block in registers as well) run one
+// wavefront per SIMD with the full register file.
 template <typename T, int DP, int DVP, int MASK, bool VARLEN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASK ? 1 : 2, 2)))
 void fused_attn_kernel(FusedArgs a) {
@@ -299,31 +299,39 @@ void fused_attn_kernel(FusedArgs a) {
   auto scores = [&](int buf, int blk, int hb) {
     const int nb = blk * kFusedBN + 32 * hb + 4 * hf;
     // mask values of the 16 keys, fetched before the MFMAs
-    float mv[16];
+    // Raw mask words of the 16 keys (fetched before the MFMAs): MASK 1 -> mw[j] holds the four
+    // bytes of keys nb + 8j .. + 3; MASK 2 -> mw[2j], mw[2j+1] their four 16-bit values.  Keys
+    // at or past the limit read as 0 (they are masked out by the limit test anyway).
+    uint32_t mw[MASK == 2 ? 8 : 4];
     if constexpr (MASK != 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n0 = nb + 8 * j;
         if (mvec && n0 + 3 < lim) {
           if constexpr (MASK == 1) {
-            const uint32_t x = *reinterpret_cast<const uint32_t*>(mrow + n0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mv[4 * j + e] = ((x >> (8 * e)) & 0xffu) ? 0.f : -INFINITY;
+            mw[j] = *reinterpret_cast<const uint32_t*>(mrow + n0);
           } else {
             const u32x2_t x = *reinterpret_cast<const u32x2_t*>(mrow + E * n0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mv[4 * j + e] = Num<T>::from_bits((x[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+            mw[2 * j] = x[0];
+            mw[2 * j + 1] = x[1];
           }
         } else {
+          uint32_t wv[2] = {0u, 0u};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int n = n0 + e;
             if (n < lim) {
-              if constexpr (MASK == 1) mv[4 * j + e] = reinterpret_cast<const uint8_t*>(mrow)[(int64_t)n * a.mJ] ? 0.f : -INFINITY;
-              else mv[4 * j + e] = Num<T>::load(reinterpret_cast<const T*>(mrow) + (int64_t)n * a.mJ);
-            } else {
-              mv[4 * j + e] = 0.f;
+              if constexpr (MASK == 1)
+                wv[0] |= (uint32_t)(reinterpret_cast<const uint8_t*>(mrow)[(int64_t)n * a.mJ] != 0) << (8 * e);
+              else
+                wv[e >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(mrow)[(int64_t)n * a.mJ] << (16 * (e & 1));
             }
+          }
+          if constexpr (MASK == 1) {
+            mw[j] = wv[0];
+          } else {
+            mw[2 * j] = wv[0];
+            mw[2 * j + 1] = wv[1];
           }
         }
       }
@@ -355,11 +363,13 @@ void fused_attn_kernel(FusedArgs a) {
           s1 = o + 1 < rel ? s1 : -INFINITY;
         }
         if constexpr (MASK == 1) {
-          s0 += mv[r];  // 0 (keep) or -inf
-          s1 += mv[r + 1];
+          const uint32_t wj = mw[r >> 2];
+          s0 = (wj >> (8 * (r & 3))) & 0xffu ? s0 : -INFINITY;
+          s1 = (wj >> (8 * ((r + 1) & 3))) & 0xffu ? s1 : -INFINITY;
         } else if constexpr (MASK == 2) {
-          s0 += mv[r];
-          s1 += mv[r + 1];
+          const uint32_t wj = mw[2 * (r >> 2) + ((r & 3) >> 1)];  // keys r, r + 1 share a word
+          s0 += Num<T>::from_bits(wj & 0xffffu);
+          s1 += Num<T>::from_bits(wj >> 16);
           round2<T>(s0, s1);
         }
         sc[r] = s0;
