@@ -166,12 +166,19 @@ int biops_conv(int dtype, int nd, int transposed, int64_t batch, int64_t cin, co
  * reference has one eager path); callers pick the fused or the materialised entry with it. */
 int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv);
 
+/* 1 when biops_sdpa_fused takes this attention mask: unit stride between keys, batch / head /
+ * query strides multiples of 4, lk a multiple of 4 and the base aligned to four elements (the
+ * kernel reads four keys at once); 0 otherwise.  No reference counterpart. */
+int biops_attention_fused_mask_ok(const void* mask, int mask_dtype, int64_t lk, int64_t mB, int64_t mH,
+                                  int64_t mI, int64_t mJ);
+
 /* Same operator and arguments as biops_sdpa, without a score matrix in memory and without a
  * workspace: each 128-row query tile walks 64-key blocks in order twice (row max and sum, then
  * P V), with the roundings of the eager composite (S, S*scale, S+mask and the normalised P
  * rounded to dtype).  S is bitwise the materialised S; the row sum may differ from the row
  * kernel's in the last fp32 bits.  Needs biops_attention_fused_supported, 16-byte aligned q/k/v
- * and strides that are multiples of 8 elements (BIOPS_ERR_LAYOUT otherwise).
+ * and strides that are multiples of 8 elements, and a mask (if any) that
+ * biops_attention_fused_mask_ok accepts (BIOPS_ERR_LAYOUT otherwise).
  * Replaces scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1148-1213). */
 int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
                      int64_t d, int64_t dv,

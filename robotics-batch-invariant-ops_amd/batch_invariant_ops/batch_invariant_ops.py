@@ -552,7 +552,10 @@ def scaled_dot_product_attention_batch_invariant(
     if out.numel() == 0:
         return out.reshape(*leading, Lq, Dv)
     causal_code = nat.CAUSAL_TOP_LEFT if is_causal else nat.CAUSAL_NONE
-    if _fused_attention_ok(query.dtype, D, Dv, q4, k4, v4):
+    fused = _fused_attention_ok(query.dtype, D, Dv, q4, k4, v4)
+    if fused and mask4 is not None:
+        fused = bool(nat.load().biops_attention_fused_mask_ok(mask4.data_ptr(), mask_code, Lk, *mask4.stride()))
+    if fused:
         nat.call(
             "biops_sdpa_fused",
             nat.dtype_code(query.dtype), B, Hq, Hkv, Lq, Lk, D, Dv,

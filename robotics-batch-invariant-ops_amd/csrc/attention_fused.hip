@@ -157,11 +157,9 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
   else return (uint32_t)Num<T>::to_bits(x) | ((uint32_t)Num<T>::to_bits(y) << 16);
 }
 
-// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD
-// without a mask; the masked kernels (mask words of a block in registers as well) run one
-// wavefront per SIMD with the full register file.
+// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD.
 template <typename T, int DP, int DVP, int MASK, bool VARLEN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASK ? 1 : 2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fused_attn_kernel(FusedArgs a) {
   using F = FusedTile<T, DP, DVP>;
   __shared__ __attribute__((aligned(16))) char smem[F::LDS_BYTES];
@@ -289,9 +287,6 @@ void fused_attn_kernel(FusedArgs a) {
 
   // Smallest key limit among the wavefront's rows: key half-blocks below it need no limit test.
   const int wave_min_lim = wrows > 0 ? row_lim(32 * w) : 0;
-  // Mask rows read 4 consecutive keys at once when they are contiguous and aligned.
-  const bool mvec = MASK != 0 && a.mJ == 1 && ((reinterpret_cast<uintptr_t>(a.mask) & 7) == 0) &&
-                    ((a.mB | a.mH | a.mI) & 3) == 0;
 
   // Transformed scores of keys 32 hb .. 32 hb + 31 of block blk: sc[r] is key
   // 64 blk + 32 hb + 8(r/4) + 4 hf + r%4 of this lane's row.
@@ -300,39 +295,22 @@ void fused_attn_kernel(FusedArgs a) {
     const int nb = blk * kFusedBN + 32 * hb + 4 * hf;
     // mask values of the 16 keys, fetched before the MFMAs
     // Raw mask words of the 16 keys (fetched before the MFMAs): MASK 1 -> mw[j] holds the four
-    // bytes of keys nb + 8j .. + 3; MASK 2 -> mw[2j], mw[2j+1] their four 16-bit values.  Keys
-    // at or past the limit read as 0 (they are masked out by the limit test anyway).
+    // bytes of keys nb + 8j .. + 3; MASK 2 -> mw[2j], mw[2j+1] their four 16-bit values.  The
+    // launcher guarantees contiguous, aligned mask rows and lk % 4 == 0, so a group of four keys
+    // starting below the limit lies inside the row; groups at or past the limit read as 0 (they
+    // are masked out by the limit test anyway).
     uint32_t mw[MASK == 2 ? 8 : 4];
     if constexpr (MASK != 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n0 = nb + 8 * j;
-        if (mvec && n0 + 3 < lim) {
-          if constexpr (MASK == 1) {
-            mw[j] = *reinterpret_cast<const uint32_t*>(mrow + n0);
-          } else {
-            const u32x2_t x = *reinterpret_cast<const u32x2_t*>(mrow + E * n0);
-            mw[2 * j] = x[0];
-            mw[2 * j + 1] = x[1];
-          }
+        const bool in = n0 < lim;
+        if constexpr (MASK == 1) {
+          mw[j] = in ? *reinterpret_cast<const uint32_t*>(mrow + n0) : 0u;
         } else {
-          uint32_t wv[2] = {0u, 0u};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int n = n0 + e;
-            if (n < lim) {
-              if constexpr (MASK == 1)
-                wv[0] |= (uint32_t)(reinterpret_cast<const uint8_t*>(mrow)[(int64_t)n * a.mJ] != 0) << (8 * e);
-              else
-                wv[e >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(mrow)[(int64_t)n * a.mJ] << (16 * (e & 1));
-            }
-          }
-          if constexpr (MASK == 1) {
-            mw[j] = wv[0];
-          } else {
-            mw[2 * j] = wv[0];
-            mw[2 * j + 1] = wv[1];
-          }
+          const u32x2_t x = in ? *reinterpret_cast<const u32x2_t*>(mrow + E * n0) : u32x2_t{0u, 0u};
+          mw[2 * j] = x[0];
+          mw[2 * j + 1] = x[1];
         }
       }
     }
@@ -523,6 +501,13 @@ extern "C" int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv)
          dv <= 128 && mult8(d) && mult8(dv);
 }
 
+extern "C" int biops_attention_fused_mask_ok(const void* mask, int mask_dtype, int64_t lk, int64_t mB,
+                                             int64_t mH, int64_t mI, int64_t mJ) {
+  const int64_t align = mask_dtype == BIOPS_BOOL ? 4 : 8;  // bytes of four mask elements
+  return mask != nullptr && mJ == 1 && lk % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) % align) == 0 &&
+         ((mB | mH | mI) & 3) == 0;
+}
+
 extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq,
                                 int64_t lk, int64_t d, int64_t dv, const void* q, int64_t sqB,
                                 int64_t sqH, int64_t sqL, const void* k, int64_t skB, int64_t skH,
@@ -537,6 +522,8 @@ extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hk
   if (mask && mask_dtype != BIOPS_BOOL && mask_dtype != dtype)
     return fail(BIOPS_ERR_DTYPE, "mask dtype must be bool or the score dtype");
   if (batch == 0 || hq == 0 || lq == 0) return BIOPS_OK;
+  if (mask && !biops_attention_fused_mask_ok(mask, mask_dtype, lk, mB, mH, mI, mJ))
+    return fail(BIOPS_ERR_LAYOUT, "fused attention needs a mask with contiguous, aligned rows and keys % 4 == 0");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !mult8(sqB) || !mult8(sqH) || !mult8(sqL) ||
       !mult8(skB) || !mult8(skH) || !mult8(skL) || !mult8(svB) || !mult8(svH) || !mult8(svL))
     return fail(BIOPS_ERR_LAYOUT, "fused attention needs 16-byte aligned rows (strides multiples of 8)");

@@ -110,6 +110,35 @@ def test_host_validation_needs_no_gpu():
     assert L.biops_reduce(0, 2, 2, 4, 8, 1, 16, 8, 2, 1, 16, null) == 2  # strided rows with K == 1
 
 
+def test_fused_attention_envelope_and_host_checks():
+    """The fused-attention entry points validate dtype, head sizes, layouts and masks on the
+    host and return their status before any launch."""
+    L = lib()
+    assert L.biops_attention_fused_supported(nat.BF16, 128, 128) == 1
+    assert L.biops_attention_fused_supported(nat.F16, 8, 8) == 1
+    assert L.biops_attention_fused_supported(nat.F32, 64, 64) == 0
+    assert L.biops_attention_fused_supported(nat.BF16, 72, 130) == 0
+    assert L.biops_attention_fused_supported(nat.BF16, 12, 64) == 0
+    # masks: unit key stride, strides and lk multiples of 4, base aligned to four elements
+    assert L.biops_attention_fused_mask_ok(64, nat.BF16, 1024, 1024 * 1024, 0, 1024, 1) == 1
+    assert L.biops_attention_fused_mask_ok(4, nat.BOOL, 1024, 1024 * 1024, 0, 1024, 1) == 1
+    assert L.biops_attention_fused_mask_ok(4, nat.BF16, 1024, 0, 0, 1024, 1) == 0  # base not 8-byte aligned
+    assert L.biops_attention_fused_mask_ok(64, nat.BF16, 1022, 0, 0, 1022, 1) == 0  # keys % 4
+    assert L.biops_attention_fused_mask_ok(64, nat.BF16, 1024, 0, 0, 1, 1024) == 0  # keys not contiguous
+    assert L.biops_attention_fused_mask_ok(None, nat.BF16, 1024, 0, 0, 1024, 1) == 0
+    p = 256  # a 16-byte aligned stand-in address: every call below fails before touching memory
+    args = [p, 0, 0, 128] * 3
+    # fp32 is outside the envelope; an odd row stride is a layout error; mask with causal
+    assert L.biops_sdpa_fused(nat.F32, 1, 1, 1, 4, 4, 128, 128, *args, None, 0, 0, 0, 0, 0, 0, 1.0, p, None) == 3
+    bad = [p, 0, 0, 130] + [p, 0, 0, 128] * 2
+    assert L.biops_sdpa_fused(nat.BF16, 1, 1, 1, 4, 4, 128, 128, *bad, None, 0, 0, 0, 0, 0, 0, 1.0, p, None) == 2
+    assert L.biops_sdpa_fused(nat.BF16, 1, 1, 1, 4, 4, 128, 128, *args, p, nat.BOOL, 0, 0, 4, 1, 1, 1.0, p, None) == 1
+    assert L.biops_sdpa_fused(nat.BF16, 1, 4, 3, 4, 4, 128, 128, *args, None, 0, 0, 0, 0, 0, 0, 1.0, p, None) == 1
+    # a mask the fused kernel cannot read four keys at a time from
+    assert L.biops_sdpa_fused(nat.BF16, 1, 1, 1, 4, 6, 128, 128, *args, p, nat.BOOL, 0, 0, 6, 1, 0, 1.0, p, None) == 2
+    assert L.biops_sdpa_fused(nat.BF16, 0, 1, 1, 4, 4, 128, 128, *args, None, 0, 0, 0, 0, 0, 0, 1.0, p, None) == 0
+
+
 def test_workspace_queries():
     L = lib()
     assert L.biops_sdpa_workspace_size(2, 16, 16, 1024, 1024) == 16 * 16 * 1024 * 1024 * 2

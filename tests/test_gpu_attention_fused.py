@@ -113,18 +113,22 @@ def test_fused_sdpa_is_batch_invariant(dtype, batch_size, causal):
 
 @pytest.mark.parametrize("mask_kind", ("boolean", "additive"))
 @pytest.mark.parametrize("dtype", DTYPES16)
-def test_fused_sdpa_masks(mask_kind, dtype, materialized):
+@pytest.mark.parametrize("lk", (172, 170))  # 170 keys: not a multiple of 4, materialised path
+def test_fused_sdpa_masks(mask_kind, dtype, lk, materialized):
     q = randn(2, 4, 150, 64, seed=8200, dtype=dtype)
-    k = randn(2, 4, 170, 64, seed=8201, dtype=dtype)
-    v = randn(2, 4, 170, 64, seed=8202, dtype=dtype)
+    k = randn(2, 4, lk, 64, seed=8201, dtype=dtype)
+    v = randn(2, 4, lk, 64, seed=8202, dtype=dtype)
     g = torch.Generator().manual_seed(8203)
-    keep = torch.rand(2, 1, 150, 170, generator=g) > 0.2
+    keep = torch.rand(2, 1, 150, lk, generator=g) > 0.2
     keep[:, :, 7] = False  # fully masked rows -> 0
     if mask_kind == "boolean":
         mask = keep
     else:
-        mask = (torch.rand(2, 1, 150, 170, generator=g) * -10).to(dtype)
+        mask = (torch.rand(2, 1, 150, lk, generator=g) * -10).to(dtype)
         mask[~keep] = -math.inf
+    assert nat.load().biops_attention_fused_mask_ok(
+        mask.cuda().data_ptr(), nat.BOOL if mask_kind == "boolean" else nat.dtype_code(dtype), lk,
+        0, 0, lk, 1) == (lk % 4 == 0)
     out = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=mask.cuda())
     check_attention(out, oracle.sdpa(q, k, v, attn_mask=mask), v, dtype)
     assert torch.count_nonzero(out[:, :, 7]) == 0
