@@ -288,19 +288,30 @@ void fused_attn_kernel(FusedArgs a) {
   // Smallest key limit among the wavefront's rows: key half-blocks below it need no limit test.
   const int wave_min_lim = wrows > 0 ? row_lim(32 * w) : 0;
 
-  // Transformed scores of keys 32 hb .. 32 hb + 31 of block blk: sc[r] is key
-  // 64 blk + 32 hb + 8(r/4) + 4 hf + r%4 of this lane's row.
-  f32x16_t sc;
-  auto scores = [&](int buf, int blk, int hb) {
-    const int nb = blk * kFusedBN + 32 * hb + 4 * hf;
-    // mask values of the 16 keys, fetched before the MFMAs
-    // Raw mask words of the 16 keys (fetched before the MFMAs): MASK 1 -> mw[j] holds the four
-    // bytes of keys nb + 8j .. + 3; MASK 2 -> mw[2j], mw[2j+1] their four 16-bit values.  The
-    // launcher guarantees contiguous, aligned mask rows and lk % 4 == 0, so a group of four keys
-    // starting below the limit lies inside the row; groups at or past the limit read as 0 (they
-    // are masked out by the limit test anyway).
-    uint32_t mw[MASK == 2 ? 8 : 4];
+  // Scores of keys 32 hb .. 32 hb + 31 of a block: acc[r] is key 64 blk + 32 hb + 8(r/4) +
+  // 4 hf + r%4 of this lane's row.  s_mfma produces the raw fp32 S (one MFMA chain over the
+  // head dimension); transform applies the reference's roundings and masks in place.
+  auto s_mfma = [&](int buf, int hb, f32x16_t& acc) {
+    const char* kb = kbuf0 + buf * F::K_BYTES;
+    {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, hf));
+      acc = mfma_first<T>(kf, qf[0]);
+    }
+#pragma unroll
+    for (int cc = 1; cc < F::QF; ++cc) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf));
+      Mfma<T>::step(acc, kf, qf[cc]);
+    }
+  };
+  // Raw mask words of the 16 keys of a half-block: MASK 1 -> mw[j] holds the four bytes of keys
+  // nb + 8j .. + 3; MASK 2 -> mw[2j], mw[2j+1] their four 16-bit values.  The launcher
+  // guarantees contiguous, aligned mask rows and lk % 4 == 0, so a group of four keys starting
+  // below the limit lies inside the row; groups at or past the limit read as 0 (they are
+  // masked out by the limit test anyway).
+  constexpr int MW = MASK == 2 ? 8 : 4;
+  auto mask_words = [&](int blk, int hb, uint32_t (&mw)[MW]) {
     if constexpr (MASK != 0) {
+      const int nb = blk * kFusedBN + 32 * hb + 4 * hf;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n0 = nb + 8 * j;
@@ -314,54 +325,60 @@ void fused_attn_kernel(FusedArgs a) {
         }
       }
     }
-    const char* kb = kbuf0 + buf * F::K_BYTES;
-    {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, hf));
-      sc = mfma_first<T>(kf, qf[0]);
-    }
-#pragma unroll
-    for (int cc = 1; cc < F::QF; ++cc) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf));
-      Mfma<T>::step(sc, kf, qf[cc]);
-    }
-    // Keys 8(r/4) + r%4 (relative to nb) at or past rel = lim - nb are masked out; when every
-    // key of the half-block is visible to every row of the wavefront the test is skipped.
-    const int rel = lim - nb;
-    auto transform = [&](auto all_visible) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float s0 = sc[r], s1 = sc[r + 1];
-        round2<T>(s0, s1);
-        s0 *= a.scale;
-        s1 *= a.scale;
-        round2<T>(s0, s1);
-        if constexpr (!decltype(all_visible)::value) {
-          const int o = 8 * (r >> 2) + (r & 3);
-          s0 = o < rel ? s0 : -INFINITY;
-          s1 = o + 1 < rel ? s1 : -INFINITY;
-        }
-        if constexpr (MASK == 1) {
-          const uint32_t wj = mw[r >> 2];
-          s0 = (wj >> (8 * (r & 3))) & 0xffu ? s0 : -INFINITY;
-          s1 = (wj >> (8 * ((r + 1) & 3))) & 0xffu ? s1 : -INFINITY;
-        } else if constexpr (MASK == 2) {
-          const uint32_t wj = mw[2 * (r >> 2) + ((r & 3) >> 1)];  // keys r, r + 1 share a word
-          s0 += Num<T>::from_bits(wj & 0xffffu);
-          s1 += Num<T>::from_bits(wj >> 16);
-          round2<T>(s0, s1);
-        }
-        sc[r] = s0;
-        sc[r + 1] = s1;
-      }
-    };
-    if (blk * kFusedBN + 32 * hb + 32 <= wave_min_lim) transform(std::true_type{});
-    else transform(std::false_type{});
   };
+  // Keys 8(r/4) + r%4 (relative to nb) at or past rel = lim - nb are masked out; OPEN skips the
+  // test (every key of the half-block is visible to every row of the wavefront).
+  auto transform = [&](auto open, int blk, int hb, f32x16_t& acc, const uint32_t (&mw)[MW]) {
+    const int rel = lim - (blk * kFusedBN + 32 * hb + 4 * hf);
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      float s0 = acc[r], s1 = acc[r + 1];
+      round2<T>(s0, s1);
+      s0 *= a.scale;
+      s1 *= a.scale;
+      round2<T>(s0, s1);
+      if constexpr (!decltype(open)::value) {
+        const int o = 8 * (r >> 2) + (r & 3);
+        s0 = o < rel ? s0 : -INFINITY;
+        s1 = o + 1 < rel ? s1 : -INFINITY;
+      }
+      if constexpr (MASK == 1) {
+        const uint32_t wj = mw[r >> 2];
+        s0 = (wj >> (8 * (r & 3))) & 0xffu ? s0 : -INFINITY;
+        s1 = (wj >> (8 * ((r + 1) & 3))) & 0xffu ? s1 : -INFINITY;
+      } else if constexpr (MASK == 2) {
+        const uint32_t wj = mw[2 * (r >> 2) + ((r & 3) >> 1)];  // keys r, r + 1 share a word
+        s0 += Num<T>::from_bits(wj & 0xffffu);
+        s1 += Num<T>::from_bits(wj >> 16);
+        round2<T>(s0, s1);
+      }
+      acc[r] = s0;
+      acc[r + 1] = s1;
+    }
+  };
+  // A half-block's state of the wavefront: skipped (no row sees a key), open or limited.
+  auto half_open = [&](int blk, int hb) { return blk * kFusedBN + 32 * hb + 32 <= wave_min_lim; };
+  auto half_live = [&](int blk, int hb) { return blk * kFusedBN + 32 * hb < wave_lim; };
 
   // ---------------------------------------------------------------- pass 1: m, l ----
   // Running maximum m (shared by both half-wavefronts of a row) and this half's sum l of
   // exp(s - m), rescaled when m grows; 32-key steps in order.
   float m = -INFINITY, l = 0.f;
+  auto stats = [&](const f32x16_t& sc) {
+    float bm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    // m = -inf until a visible key appears: the shift stays 0 and every term is exp(-inf) = 0
+    const float mn = fmaxf(m, bm);
+    const float sh = (mn == -INFINITY ? 0.f : mn) * kLog2e;
+    const float corr = __builtin_amdgcn_exp2f(m * kLog2e - sh);
+    float part = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kLog2e, -sh));
+    l = l * corr + part;
+    m = mn;
+  };
   if (nblk > 0) {
     load_k(0);
     store_k(0);
@@ -369,23 +386,31 @@ void fused_attn_kernel(FusedArgs a) {
   }
   for (int blk = 0; blk < nblk; ++blk) {
     if (blk + 1 < nblk) load_k(blk + 1);
+    const int buf = blk & 1;
+    if (half_open(blk, 1)) {
+      // both halves open: the second S chain overlaps the first half's vector work
+      uint32_t mw0[MW], mw1[MW];
+      mask_words(blk, 0, mw0);
+      mask_words(blk, 1, mw1);
+      f32x16_t s0, s1;
+      s_mfma(buf, 0, s0);
+      s_mfma(buf, 1, s1);
+      transform(std::true_type{}, blk, 0, s0, mw0);
+      stats(s0);
+      transform(std::true_type{}, blk, 1, s1, mw1);
+      stats(s1);
+    } else {
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      if (blk * kFusedBN + 32 * hb < wave_lim) {
-        scores(blk & 1, blk, hb);
-        float bm = sc[0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        // m = -inf until a visible key appears: the shift stays 0 and every term is exp(-inf) = 0
-        const float mn = fmaxf(m, bm);
-        const float sh = (mn == -INFINITY ? 0.f : mn) * kLog2e;
-        const float corr = __builtin_amdgcn_exp2f(m * kLog2e - sh);
-        float part = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kLog2e, -sh));
-        l = l * corr + part;
-        m = mn;
+      for (int hb = 0; hb < 2; ++hb) {
+        if (half_live(blk, hb)) {
+          uint32_t mw[MW];
+          mask_words(blk, hb, mw);
+          f32x16_t sc;
+          s_mfma(buf, hb, sc);
+          if (half_open(blk, hb)) transform(std::true_type{}, blk, hb, sc, mw);
+          else transform(std::false_type{}, blk, hb, sc, mw);
+          stats(sc);
+        }
       }
     }
     if (blk + 1 < nblk) store_k((blk + 1) & 1);
@@ -413,33 +438,56 @@ void fused_attn_kernel(FusedArgs a) {
   // column n0 + 4(s%4), and receives rows k0..k0+3 of column n0 + s.
   const int vrow = 4 * hf + ((lane & 15) >> 2);
   const int vcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // P = round(exp(s - m) / l) of a half-block's two 16-key chunks, each straight into PV MFMAs.
+  auto pv = [&](const f32x16_t& sc, int hb, const char* vb) {
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      // 16-key chunk c = 2 hb + c2: this lane's keys 16c + 4hf + (0..3) and + 8
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * c2 + e], kLog2e, -shl2e)) * inv;
+      const u32x4_t pa = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
+                          pack2<T>(p[6], p[7])};
+      const int row = 16 * (2 * hb + c2) + vrow;
+#pragma unroll
+      for (int e = 0; e < F::OF; ++e) {
+        const u32x2_t lo = lds_read_tr16(vb + F::v_off(row, 32 * e + vcol));
+        const u32x2_t hi = lds_read_tr16(vb + F::v_off(row + 8, 32 * e + vcol));
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        Mfma<T>::step(oacc[e], pa, vf);
+      }
+    }
+  };
   for (int blk = 0; blk < nblk; ++blk) {
     if (blk + 1 < nblk) {
       load_k(blk + 1);
       load_v(blk + 1);
     }
-    const char* vb = vbuf0 + (blk & 1) * F::V_BYTES;
+    const int buf = blk & 1;
+    const char* vb = vbuf0 + buf * F::V_BYTES;
+    if (half_open(blk, 1)) {
+      uint32_t mw0[MW], mw1[MW];
+      mask_words(blk, 0, mw0);
+      mask_words(blk, 1, mw1);
+      f32x16_t s0, s1;
+      s_mfma(buf, 0, s0);
+      s_mfma(buf, 1, s1);
+      transform(std::true_type{}, blk, 0, s0, mw0);
+      pv(s0, 0, vb);
+      transform(std::true_type{}, blk, 1, s1, mw1);
+      pv(s1, 1, vb);
+    } else {
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      if (blk * kFusedBN + 32 * hb < wave_lim) {
-        scores(blk & 1, blk, hb);
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          // 16-key chunk c = 2 hb + c2: this lane's keys 16c + 4hf + (0..3) and + 8
-          float p[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * c2 + e], kLog2e, -shl2e)) * inv;
-          const u32x4_t pa = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
-                              pack2<T>(p[6], p[7])};
-          const int row = 16 * (2 * hb + c2) + vrow;
-#pragma unroll
-          for (int e = 0; e < F::OF; ++e) {
-            const u32x2_t lo = lds_read_tr16(vb + F::v_off(row, 32 * e + vcol));
-            const u32x2_t hi = lds_read_tr16(vb + F::v_off(row + 8, 32 * e + vcol));
-            const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-            Mfma<T>::step(oacc[e], pa, vf);
-          }
+      for (int hb = 0; hb < 2; ++hb) {
+        if (half_live(blk, hb)) {
+          uint32_t mw[MW];
+          mask_words(blk, hb, mw);
+          f32x16_t sc;
+          s_mfma(buf, hb, sc);
+          if (half_open(blk, hb)) transform(std::true_type{}, blk, hb, sc, mw);
+          else transform(std::false_type{}, blk, hb, sc, mw);
+          pv(sc, hb, vb);
         }
       }
     }
