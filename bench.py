@@ -70,6 +70,20 @@ def profile_kernel(which, iters):
         v = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).cuda()
         for _ in range(iters):
             bio.scaled_dot_product_attention_batch_invariant(q, k, v, is_causal=True, enable_gqa=True)
+    elif which == "moe":
+        # configs[4] at T = 4096, selected routes (the default evaluation)
+        from batch_invariant_ops.moe import _moe
+
+        g = torch.Generator().manual_seed(5)
+        hidden = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).cuda()
+        gu = (torch.randn(64, 2048, 1536, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        dn = (torch.randn(64, 768, 2048, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        probs = torch.softmax(torch.randn(4096, 64, generator=g), -1)
+        wts, sel = torch.topk(probs, 8, dim=-1)
+        wts, sel = wts.cuda(), sel.cuda()
+        for _ in range(iters):
+            _moe(hidden, wts, sel, gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2),
+                 dn.transpose(1, 2), sparse=True)
     elif which == "softmax":
         x = torch.randn(16 * 16 * 1024, 1024, device="cuda").to(torch.bfloat16)
         for _ in range(iters):
@@ -102,11 +116,12 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "copy", "sdpa", "softmax", "norm"),
+        choices=("gemm", "copy", "sdpa", "moe", "softmax", "norm"),
         default=None,
         help="only launch the roofline kernel (gemm), a 512 MiB device copy (copy), configs[2] "
-        "causal attention at B=16 (sdpa), a 262144x1024 bf16 softmax (softmax) or a 65536x2048 "
-        "bf16 row L2 norm (norm) --iters times, for counter runs; prints no JSON line",
+        "causal attention at B=16 (sdpa), configs[4] MoE at T=4096 (moe), a 262144x1024 bf16 "
+        "softmax (softmax) or a 65536x2048 bf16 row L2 norm (norm) --iters times, for counter "
+        "runs; prints no JSON line",
     )
     p.add_argument("--iters", type=int, default=10)
     return p.parse_args()
