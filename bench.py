@@ -10,7 +10,8 @@ value = sum of FLOPs / wall time of the step.  The line also carries the rooflin
 dominant kernel (M = 4096, measured alone), the bitwise B=1-vs-B=N check and a CPU baseline.
 
 --configs REPORT.json additionally runs the five BASELINE configs (BI check + throughput of
-every kernel family) and writes them to REPORT.json; the headline line is unchanged.
+every kernel family, and the reference's CPU path of each config on a bounded sample) and
+writes them to REPORT.json; the headline line is unchanged.
 """
 
 from __future__ import annotations
@@ -177,6 +178,105 @@ def cpu_baseline(seconds):
         "sample": f"oracle.linear (torch {torch.__version__} CPU, fp64 accumulate, bf16 rounding) "
         f"on M=256 rows of both configs[1] linears, {reps} reps in {dt:.1f}s",
     }
+
+
+def _cpu_time(fn, seconds):
+    """Median seconds per call of fn() on the host (at least 2 calls, about `seconds` total)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_config_baselines(seconds=3.0):
+    """The reference's CPU path for every BASELINE config: stock torch CPU ops with the mode off
+    (what batch_invariant_ops does without a GPU), timed on bounded samples of each workload.
+    Each entry gives the sample, the median time per call and the rate in the config's unit."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    out = {"cores": cores, "torch": torch.__version__, "kind": "reference CPU path (stock torch ops)"}
+    bf = torch.bfloat16
+
+    a = torch.linspace(-100, 100, 2048 * 4096).reshape(2048, 4096)
+    b = torch.linspace(-100, 100, 4096 * 4096).reshape(4096, 4096)
+    t, n = _cpu_time(lambda: torch.mm(a, b), seconds)
+    out["C1_fp32_mm"] = {"sample": "full 2048x4096x4096 fp32 mm", "s_per_call": t, "calls": n,
+                         "tflops": 2 * 2048 * 4096 * 4096 / t / 1e12}
+    del a, b
+
+    g = torch.Generator().manual_seed(20)
+    x = torch.randn(1, 256, 2048, generator=g).to(bf)
+    w1 = (torch.randn(8192, 2048, generator=g) * 0.02).to(bf)
+    b1 = (torch.randn(8192, generator=g) * 0.02).to(bf)
+    w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(bf)
+
+    def stack():
+        y = F.linear(F.linear(x, w1, b1), w2)
+        var = y.float().pow(2).mean(-1, keepdim=True)
+        yn = (y.float() * torch.rsqrt(var + 1e-6)).to(bf)
+        return yn.mean(-1), torch.linalg.vector_norm(yn, dim=-1)
+
+    t, n = _cpu_time(stack, seconds)
+    out["C2_linear_rmsnorm"] = {"sample": "B=1 (M=256): both linears + RMSNorm + mean + vector_norm, bf16",
+                                "s_per_call": t, "calls": n, "gemm_tflops": 2 * 2 * 256 * 8192 * 2048 / t / 1e12}
+    del x, w1, b1, w2
+
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 16, 1024, 128, generator=g).to(bf)
+    k = torch.randn(1, 4, 1024, 128, generator=g).to(bf)
+    v = torch.randn(1, 4, 1024, 128, generator=g).to(bf)
+    t, n = _cpu_time(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True), seconds)
+    out["C3_sdpa"] = {"sample": "B=1 causal, GQA 16/4, L=1024, D=128, bf16", "s_per_call": t, "calls": n,
+                      "tflops_useful": 4 * 16 * 128 * 1024 * 1025 / 2 / t / 1e12}
+    del q, k, v
+
+    g = torch.Generator().manual_seed(4)
+    lengths = torch.randint(64, 2049, (32,), generator=g)[:4]
+    seqs = [(torch.randn(1, 8, int(L), 64, generator=g).to(bf), torch.randn(1, 2, int(L), 64, generator=g).to(bf))
+            for L in lengths]
+
+    def varlen_loop():
+        for qq, kk in seqs:
+            F.scaled_dot_product_attention(qq, kk, kk, is_causal=True, enable_gqa=True)
+
+    t, n = _cpu_time(varlen_loop, seconds)
+    pairs = float((lengths.double() * (lengths.double() + 1) / 2).sum())
+    out["C4_varlen"] = {"sample": f"per-sequence SDPA loop over 4 of the 32 sequences (lengths {lengths.tolist()})",
+                        "s_per_call": t, "calls": n, "tflops_useful": 4 * 8 * 64 * pairs / t / 1e12}
+    del seqs
+
+    g = torch.Generator().manual_seed(5)
+    T = 16
+    hidden = torch.randn(T, 2048, generator=g).to(bf)
+    gu = (torch.randn(64, 2048, 1536, generator=g) * 0.02).to(bf)
+    dn = (torch.randn(64, 768, 2048, generator=g) * 0.02).to(bf)
+    wts, sel = torch.topk(torch.softmax(torch.randn(T, 64, generator=g), -1), 8, dim=-1)
+    gate, up, down = gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2), dn.transpose(1, 2)
+
+    def moe_cpu():  # the reference's CPU branch (moe.py:75-92): dense bmm over every expert
+        xe = hidden.unsqueeze(0).expand(64, -1, -1)
+        ge = torch.bmm(xe, gate.transpose(1, 2))
+        ue = torch.bmm(xe, up.transpose(1, 2))
+        y = torch.bmm(F.silu(ge) * ue, down.transpose(1, 2)).permute(1, 0, 2)
+        r = torch.gather(y, 1, sel.unsqueeze(-1).expand(-1, -1, 2048)) * wts.unsqueeze(-1).to(bf)
+        o = r[:, 0]
+        for s_ in range(1, 8):
+            o = o + r[:, s_]
+        return o
+
+    t, n = _cpu_time(moe_cpu, seconds)
+    out["C5_moe"] = {"sample": f"T={T} tokens, dense every-expert bmm branch, bf16", "s_per_call": t, "calls": n,
+                     "dense_tflops": 6 * 64 * T * 2048 * 768 / t / 1e12,
+                     "route_tflops": 6 * 8 * T * 2048 * 768 / t / 1e12}
+    return out
 
 
 def _bitwise(a, b):
@@ -478,6 +578,8 @@ def main():
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     if args.configs:
         report = run_all()
+        if not args.no_cpu:
+            report["cpu_baselines"] = cpu_config_baselines()
         with open(args.configs, "w") as fh:
             json.dump(report, fh, indent=1)
     print(json.dumps(line), flush=True)
