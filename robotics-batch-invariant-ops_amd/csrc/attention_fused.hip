@@ -44,6 +44,9 @@ struct FusedArgs {
 
 constexpr int kFusedBM = 128;  // query rows per workgroup
 constexpr int kFusedBN = 64;   // keys per block
+// The varlen kernels take their tiles from the work list's PV tile prefix (one tile per head
+// and 128 query rows when dv <= 128).
+static_assert(kFusedBM == kVarlenBM && kVarlenBN >= 128, "fused tiles follow the varlen plan");
 
 template <typename T, int DP, int DVP>
 struct FusedTile {
@@ -605,6 +608,11 @@ extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64
   if (!dplan || !hplan) return fail(BIOPS_ERR_ARG, "null plan");
   const int64_t items = hplan[0];
   if (items == 0) return BIOPS_OK;
+  for (int64_t i = 0; i < items; ++i) {  // sequence lengths are 32-bit inside the kernel
+    const int64_t* p = hplan + kPlanHeader + kPlanStride * i;
+    if (p[1] >= (int64_t(1) << 31) || p[3] >= (int64_t(1) << 31))
+      return fail(BIOPS_ERR_LAYOUT, "fused attention sequence longer than 2^31 tokens");
+  }
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !mult8(sq_t) || !mult8(sq_h) ||
       !mult8(sk_t) || !mult8(sk_h) || !mult8(sv_t) || !mult8(sv_h))
     return fail(BIOPS_ERR_LAYOUT, "fused attention needs 16-byte aligned rows (strides multiples of 8)");

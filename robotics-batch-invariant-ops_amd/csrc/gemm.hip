@@ -234,6 +234,10 @@ void big_kernel(BmmArgs args) {
 // resident workgroups share the unit, so they do not finish sooner), and the entry with the
 // smallest estimate is launched.
 static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 910, 570, 670, 900, 900};
+// With a 16-bit N-major B on the direct path the fragments come through the transposing LDS
+// reads; measured on MI355X (M = 4096 x N = 8192 / 2048 x K = 2048 / 8192 and 2048 x 1536 x 2048)
+// each entry keeps this share of its K-major rate (small wave tiles lose the most).
+static const double kCfgNmajorShare[kNumCfg] = {0.97, 0.78, 0.86, 0.60, 0.72, 0.60, 0.55, 0.91, 0.73, 0.78, 0.80, 0.83};
 static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 256, 128, 128, 256, 128};
 static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 256, 128, 256, 128, 256};
 
@@ -271,7 +275,7 @@ static bool cfg_ok(int dtype, int c, bool swiglu, bool grouped) {
   return !swiglu || c <= 2;
 }
 
-static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
+static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool nmajor16) {
   const bool swiglu = epi == kEpiSwiglu;
   const bool grouped = a.grp != nullptr;
   const int forced = forced_cfg();
@@ -281,7 +285,7 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
   if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
   const int64_t batch = a.nb1 * a.nb2;
-  // Grouped rows: groups of the mean size, each ending in a part-filled m-tile.
+  // Grouped rows: groups of the mean size.
   const int64_t groups = std::max<int64_t>(1, std::min(a.grp_groups, a.grp_rows));
   const int64_t mean = a.grp_rows / groups;
   int best = 2;
@@ -289,9 +293,13 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok) {
   for (int c = 0; c < kNumCfg; ++c) {
     if (!cfg_ok(dtype, c, swiglu, grouped)) continue;
     const int64_t cols = swiglu ? kCfgBN[c] / 2 : kCfgBN[c];
-    const int64_t mt = grouped ? groups * (mean / kCfgBM[c] + 1) : batch * cdiv(a.M, kCfgBM[c]);
+    // grouped: a group of the mean size spans mean / BM tiles plus, on average, half a tile of
+    // its last partial m-tile (and at least one tile)
+    const double per_group = std::max((double)cdiv(mean, kCfgBM[c]), (double)mean / kCfgBM[c] + 0.5);
+    const int64_t mt = grouped ? (int64_t)(groups * per_group + 0.5) : batch * cdiv(a.M, kCfgBM[c]);
     const int64_t tiles = mt * cdiv(a.N, cols);
-    const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / kCfgRate[c];
+    const double rate = kCfgRate[c] * (nmajor16 ? kCfgNmajorShare[c] : 1.0);
+    const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / rate;
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
@@ -436,7 +444,7 @@ static int prepare_bmm(int dtype, BmmArgs& a, int epi, bool b_kmajor, bool& dire
   // Grouped rows run on the table entries only (the skinny and large-tile kernels take a fixed
   // tile count from the host); those two read K-major B only.
   const bool skinny_ok = direct && b_kmajor && epi != kEpiSwiglu && a.grp == nullptr;
-  return pick_cfg(dtype, a, epi, skinny_ok);
+  return pick_cfg(dtype, a, epi, skinny_ok, direct && !b_kmajor && elt == 2);
 }
 
 int grouped_tile_rows(int dtype, BmmArgs a, int epi, bool b_kmajor) {
