@@ -105,6 +105,8 @@ def library_path() -> pathlib.Path:
 def load(require_gpu: bool = True) -> ctypes.CDLL:
     """Load libbiops.so (once).  With ``require_gpu`` also insist on a visible ROCm GPU."""
     global _lib
+    if _lib is not None and (_gpu_seen or not require_gpu):
+        return _lib
     if require_gpu and not torch.cuda.is_available():
         raise RuntimeError(
             "batch_invariant_ops needs a ROCm GPU: torch.cuda.is_available() is False"
@@ -123,7 +125,18 @@ def load(require_gpu: bool = True) -> ctypes.CDLL:
                     fn.restype = res
                     fn.argtypes = args
                 _lib = lib
+    if require_gpu:
+        _set_gpu_seen()
     return _lib
+
+
+_gpu_seen = False
+
+
+def _set_gpu_seen() -> None:
+    """The GPU check passed once; later loads skip it (devices do not disappear)."""
+    global _gpu_seen
+    _gpu_seen = True
 
 
 def dtype_code(dtype: torch.dtype) -> int:
