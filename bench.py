@@ -403,6 +403,26 @@ def run_all():
     report["C3_sdpa"] = c3
     del q, k, v, mask
 
+    # beyond the configs: 256-wide heads (Gemma-style multi-query attention), causal, B = 4
+    g = torch.Generator().manual_seed(33)
+    q = torch.randn(4, 8, 1024, 256, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(4, 1, 1024, 256, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(4, 1, 1024, 256, generator=g).to(torch.bfloat16).to(dev)
+
+    def run256():
+        return bio.scaled_dot_product_attention_batch_invariant(q, k, v, is_causal=True, enable_gqa=True)
+
+    o = run256()
+    d256 = {"bitwise_B1_B4": _bitwise(bio.scaled_dot_product_attention_batch_invariant(
+        q[:1], k[:1], v[:1], is_causal=True, enable_gqa=True), o[:1])}
+    ms = event_time(run256, 5)
+    d256["ms"] = ms
+    d256["tflops_useful"] = 4 * 4 * 8 * 256 * 1024 * 1025 / 2 / (ms * 1e-3) / 1e12
+    with _materialized_attention():
+        d256["materialized_ms"] = event_time(run256, 5)
+    report["sdpa_head256_causal_B4_H8_MQA"] = d256
+    del q, k, v
+
     # C4: packed varlen, 32 sequences, bottom-right causal
     g = torch.Generator().manual_seed(4)
     lengths = torch.randint(64, 2049, (32,), generator=g)

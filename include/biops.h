@@ -161,10 +161,12 @@ int biops_conv(int dtype, int nd, int transposed, int64_t batch, int64_t cin, co
 
 /* ------------------------------------------------------------------- attention ---- */
 
-/* 1 when biops_sdpa_fused / biops_varlen_sdpa_fused take this dtype and head sizes: bf16 or
- * fp16, 1 <= d, dv <= 128, both multiples of 8; 0 otherwise.  No reference counterpart (the
- * reference has one eager path); callers pick the fused or the materialised entry with it. */
+/* 1 when biops_sdpa_fused takes this dtype and head sizes: bf16 or fp16, 1 <= d, dv <= 256,
+ * both multiples of 8; 0 otherwise.  biops_varlen_fused_supported: the same for
+ * biops_varlen_sdpa_fused, with d, dv <= 128.  No reference counterpart (the reference has one
+ * eager path); callers pick the fused or the materialised entry with them. */
 int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv);
+int biops_varlen_fused_supported(int dtype, int64_t d, int64_t dv);
 
 /* 1 when biops_sdpa_fused takes this attention mask: unit stride between keys, batch / head /
  * query strides multiples of 4, lk a multiple of 4 and the base aligned to four elements (the
@@ -189,7 +191,7 @@ int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t 
                      int causal, float scale, void* out, void* stream);
 
 /* Packed varlen attention with the fused kernel: same arguments as biops_varlen_sdpa without
- * the workspace (the plan from biops_varlen_plan, dv <= 128).  out rows outside every
+ * the workspace (the plan from biops_varlen_plan; biops_varlen_fused_supported).  out rows outside every
  * sequence are not written.  Same layout conditions as biops_sdpa_fused.
  * Replaces varlen_scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1216-1344). */
 int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,

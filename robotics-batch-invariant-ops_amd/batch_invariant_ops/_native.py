@@ -57,6 +57,7 @@ _SIGNATURES = {
         + [_p, _i, _l, _l, _l, _l, _i, _f, _p, _p, _l, _p],
     ),
     "biops_attention_fused_supported": (_i, [_i, _l, _l]),
+    "biops_varlen_fused_supported": (_i, [_i, _l, _l]),
     "biops_attention_fused_mask_ok": (_i, [_p, _i, _l, _l, _l, _l, _l]),
     "biops_sdpa_fused": (
         _i,

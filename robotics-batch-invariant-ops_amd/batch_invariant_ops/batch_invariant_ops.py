@@ -444,13 +444,15 @@ def linalg_vector_norm_batch_invariant(
 
 
 # -------------------------------------------------------------------- attention ----
-def _fused_attention_ok(dtype, d, dv, *tensors):
-    """True when the fused attention kernel takes this call: bf16/fp16, head sizes <= 128 and
-    multiples of 8, 16-byte aligned rows.  ``BIOPS_ATTENTION_MATERIALIZE=1`` selects the
-    materialised-score path (same operator, row sums in the row kernel's order)."""
+def _fused_attention_ok(dtype, d, dv, *tensors, varlen=False):
+    """True when the fused attention kernel takes this call: bf16/fp16, head sizes multiples of
+    8 up to 256 (128 for varlen), 16-byte aligned rows.  ``BIOPS_ATTENTION_MATERIALIZE=1``
+    selects the materialised-score path (same operator, row sums in the row kernel's order)."""
     if dtype not in (torch.bfloat16, torch.float16) or nat.env_flag("BIOPS_ATTENTION_MATERIALIZE", False):
         return False
-    if not nat.load().biops_attention_fused_supported(nat.dtype_code(dtype), d, dv):
+    lib = nat.load()
+    supported = lib.biops_varlen_fused_supported if varlen else lib.biops_attention_fused_supported
+    if not supported(nat.dtype_code(dtype), d, dv):
         return False
     for t in tensors:
         if t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:-1]):
@@ -680,7 +682,7 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     else:
         causal = nat.CAUSAL_NONE
     scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
-    if _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v):
+    if _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v, varlen=True):
         nat.call(
             "biops_varlen_sdpa_fused",
             nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,

@@ -160,9 +160,14 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
   else return (uint32_t)Num<T>::to_bits(x) | ((uint32_t)Num<T>::to_bits(y) << 16);
 }
 
-// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD.
+// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD
+// up to head size 128; with a 256-wide head (Q fragments and O accumulators twice as large,
+// 128 KiB of K/V blocks) one wavefront per SIMD with the full register file.
+template <int DP, int DVP>
+constexpr int fused_waves_per_eu() { return DP > 128 || DVP > 128 ? 1 : 2; }
+
 template <typename T, int DP, int DVP, int MASK, bool VARLEN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves_per_eu<DP, DVP>(), 2)))
 void fused_attn_kernel(FusedArgs a) {
   using F = FusedTile<T, DP, DVP>;
   __shared__ __attribute__((aligned(16))) char smem[F::LDS_BYTES];
@@ -524,6 +529,13 @@ static int launch_fused_t(const FusedArgs& a, hipStream_t s) {
 
 template <typename T, int MASK, bool VARLEN>
 static int launch_fused_d(const FusedArgs& a, hipStream_t s) {
+  if constexpr (!VARLEN) {  // 256-wide heads: dense SDPA only (the varlen plan has 128-wide PV tiles)
+    if (a.d > 128) {
+      if (a.dv <= 128) return launch_fused_t<T, 256, 128, MASK, false>(a, s);
+      return launch_fused_t<T, 256, 256, MASK, false>(a, s);
+    }
+    if (a.dv > 128) return launch_fused_t<T, 128, 256, MASK, false>(a, s);
+  }
   if (a.d <= 64) {
     if (a.dv <= 64) return launch_fused_t<T, 64, 64, MASK, VARLEN>(a, s);
     return launch_fused_t<T, 64, 128, MASK, VARLEN>(a, s);
@@ -548,8 +560,12 @@ static bool block_fits(int64_t row_stride) { return row_stride >= 0 && 2 * kFuse
 using namespace biops;
 
 extern "C" int biops_attention_fused_supported(int dtype, int64_t d, int64_t dv) {
-  return (dtype == BIOPS_BF16 || dtype == BIOPS_F16) && d >= 1 && d <= 128 && dv >= 1 &&
-         dv <= 128 && mult8(d) && mult8(dv);
+  return (dtype == BIOPS_BF16 || dtype == BIOPS_F16) && d >= 1 && d <= 256 && dv >= 1 &&
+         dv <= 256 && mult8(d) && mult8(dv);
+}
+
+extern "C" int biops_varlen_fused_supported(int dtype, int64_t d, int64_t dv) {
+  return biops_attention_fused_supported(dtype, d, dv) && d <= 128 && dv <= 128;
 }
 
 extern "C" int biops_attention_fused_mask_ok(const void* mask, int mask_dtype, int64_t lk, int64_t mB,
@@ -566,7 +582,7 @@ extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hk
                                 const void* mask, int mask_dtype, int64_t mB, int64_t mH, int64_t mI,
                                 int64_t mJ, int causal, float scale, void* out, void* stream) {
   if (!biops_attention_fused_supported(dtype, d, dv))
-    return fail(BIOPS_ERR_DTYPE, "fused attention takes bf16/fp16 with head dims <= 128, multiples of 8");
+    return fail(BIOPS_ERR_DTYPE, "fused attention takes bf16/fp16 with head dims <= 256, multiples of 8");
   if (batch < 0 || hq < 0 || hkv <= 0 || lq < 0 || lk < 0) return fail(BIOPS_ERR_ARG, "invalid attention sizes");
   if (hq % hkv != 0) return fail(BIOPS_ERR_ARG, "query heads must be a multiple of kv heads");
   if (mask && causal != BIOPS_CAUSAL_NONE) return fail(BIOPS_ERR_ARG, "mask and causal are exclusive");
@@ -602,8 +618,8 @@ extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64
                                        int64_t sv_h, void* out, int64_t so_t, int64_t so_h,
                                        const int64_t* dplan, const int64_t* hplan, int causal,
                                        float scale, void* stream) {
-  if (!biops_attention_fused_supported(dtype, d, dv))
-    return fail(BIOPS_ERR_DTYPE, "fused attention takes bf16/fp16 with head dims <= 128, multiples of 8");
+  if (!biops_varlen_fused_supported(dtype, d, dv))
+    return fail(BIOPS_ERR_DTYPE, "fused varlen attention takes bf16/fp16 with head dims <= 128, multiples of 8");
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(BIOPS_ERR_ARG, "invalid varlen head configuration");
   if (!dplan || !hplan) return fail(BIOPS_ERR_ARG, "null plan");
   const int64_t items = hplan[0];

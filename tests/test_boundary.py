@@ -118,6 +118,8 @@ def test_fused_attention_envelope_and_host_checks():
     assert L.biops_attention_fused_supported(nat.F16, 8, 8) == 1
     assert L.biops_attention_fused_supported(nat.F32, 64, 64) == 0
     assert L.biops_attention_fused_supported(nat.BF16, 72, 130) == 0
+    assert L.biops_attention_fused_supported(nat.BF16, 256, 200) == 1
+    assert L.biops_varlen_fused_supported(nat.BF16, 256, 200) == 0
     assert L.biops_attention_fused_supported(nat.BF16, 12, 64) == 0
     # masks: unit key stride, strides and lk multiples of 4, base aligned to four elements
     assert L.biops_attention_fused_mask_ok(64, nat.BF16, 1024, 1024 * 1024, 0, 1024, 1) == 1

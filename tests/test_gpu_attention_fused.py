@@ -2,7 +2,8 @@
 materialised-score path, and bitwise batch invariance (reference tests
 test_batch_invariance.py:512-742 for the operator semantics).
 
-The fused kernel takes bf16 / fp16 calls with head sizes <= 128 that are multiples of 8; the
+The fused kernel takes bf16 / fp16 calls with head sizes <= 256 (varlen: <= 128) that are
+multiples of 8; the
 shapes below cover partial query tiles (rows not a multiple of 128), partial key blocks (keys not
 a multiple of 64), head-dim padding (72 -> 128, 40 -> 64), grouped-query heads, both causal
 alignments, boolean and additive masks and fully masked rows.
@@ -62,8 +63,11 @@ def test_fused_envelope():
     assert lib.biops_attention_fused_supported(nat.F16, 8, 64) == 1
     assert lib.biops_attention_fused_supported(nat.F32, 64, 64) == 0
     assert lib.biops_attention_fused_supported(nat.BF16, 65, 64) == 0
-    assert lib.biops_attention_fused_supported(nat.BF16, 136, 64) == 0
+    assert lib.biops_attention_fused_supported(nat.BF16, 256, 256) == 1
+    assert lib.biops_attention_fused_supported(nat.BF16, 264, 64) == 0
     assert lib.biops_attention_fused_supported(nat.BF16, 64, 0) == 0
+    assert lib.biops_varlen_fused_supported(nat.BF16, 128, 128) == 1
+    assert lib.biops_varlen_fused_supported(nat.BF16, 136, 64) == 0
 
 
 SHAPES = (
@@ -74,6 +78,9 @@ SHAPES = (
     (1, 4, 1, 1, 300, 128, 64),
     (3, 2, 2, 257, 65, 32, 128),
     (1, 2, 2, 64, 1, 8, 8),
+    (2, 8, 1, 300, 257, 256, 256),   # 256-wide heads (one wavefront per SIMD)
+    (1, 4, 2, 129, 64, 200, 136),
+    (1, 2, 2, 65, 130, 96, 256),
 )
 
 
