@@ -34,6 +34,8 @@ struct BmmArgs {
   int64_t sA1, sA2, sB1, sB2, sC1, sC2;
   const int32_t* grp;
   int64_t grp_rows, grp_groups;
+  // Grouped rows only: row p of the packed problem reads A row a_rows[p] (nullptr: row p).
+  const int32_t* a_rows;
   // filled by the launcher
   int64_t tiles_m, tiles_n, total;
   int32_t a_vec, b_vec, c_vec;

@@ -126,8 +126,18 @@ __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* 
   const int64_t rows = o.m_end - m0;
   const int64_t cols = args.N - n0;
 
-  if constexpr (C::pingpong && DIRECT) Tile::mainloop_pingpong(smem, acc, A, args.lda, rows, src, args.K);
-  else Tile::mainloop(smem, acc, A, args.lda, rows, args.a_vec != 0, src, args.K);
+  auto run = [&](const auto& as) {
+    if constexpr (C::pingpong && DIRECT) Tile::mainloop_pingpong(smem, acc, as, src, args.K);
+    else Tile::mainloop(smem, acc, as, args.a_vec != 0, src, args.K);
+  };
+  if constexpr (GRP) {
+    if (args.a_rows)  // rows come through the table (grouped launches have no A batch strides)
+      run(Tile::a_table(reinterpret_cast<const T*>(args.A), args.lda, rows, args.a_rows + m0));
+    else
+      run(typename Tile::ARows{A, args.lda, rows});
+  } else {
+    run(typename Tile::ARows{A, args.lda, rows});
+  }
 
   T* Cp = reinterpret_cast<T*>(args.C) + b1 * args.sC1 + b2 * args.sC2 + m0 * args.ldc + n0;
   const T* bias = (EPI != kEpiSwiglu && args.bias) ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
@@ -565,7 +575,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
     src.swiglu = false;
     const int64_t rows = M - m0, cols = N - n0;
 
-    Tile::mainloop(smem, acc, A, lda, rows, avec, src, K);
+    Tile::mainloop(smem, acc, typename Tile::ARows{A, lda, rows}, avec, src, K);
     const bool cvec = al(C, 0) && (ldc * elt) % 16 == 0;
     Tile::template epilogue<false>(smem, acc, C, ldc, rows < BM ? (int)rows : BM,
                                    cols < BN ? (int)cols : BN, nullptr, cvec);

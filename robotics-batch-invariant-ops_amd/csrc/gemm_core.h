@@ -162,8 +162,46 @@ struct GemmTile {
   };
 
   // ---------------------------------------------------------------- register path ----
-  __device__ static __forceinline__ void reg_load_a(Regs& R, const T* A, int64_t lda, int64_t rows,
-                                                    int64_t k0, int64_t K, bool vec_ok) {
+  // Where the tile's A rows come from.  ARows: row r (clamped to rows - 1 for the direct
+  // loads) at A + r * lda, addresses formed per call.  ATable: row r at A + idx[r] * lda (a
+  // row table, grouped launches), with this thread's direct-load sources read from the table
+  // once per tile.  at(p) is the source of direct-load slot s = t + THREADS*p at K = 0: row s/8,
+  // logical chunk (s%8) ^ ((row>>1)&7).
+  __device__ static __forceinline__ int slot_row(int p) { return (threadIdx.x + THREADS * p) >> 3; }
+  __device__ static __forceinline__ int slot_chunk(int p) {
+    const int s = threadIdx.x + THREADS * p;
+    return (s & 7) ^ (((s >> 3) >> 1) & 7);
+  }
+  struct ARows {
+    const T* A;
+    int64_t lda, rows;
+    __device__ __forceinline__ const T* row_ptr(int64_t r) const { return A + r * lda; }
+    __device__ __forceinline__ const T* at(int p) const {
+      const int r = slot_row(p);
+      return row_ptr(r < rows ? r : rows - 1) + slot_chunk(p) * VEC;
+    }
+  };
+  static constexpr int A_DIRECT = A_SLOTS / THREADS > 0 ? A_SLOTS / THREADS : 1;
+  struct ATable {
+    const T* A;
+    int64_t lda, rows;
+    const int32_t* idx;
+    const T* src[A_DIRECT];
+    __device__ __forceinline__ const T* row_ptr(int64_t r) const { return A + (int64_t)idx[r] * lda; }
+    __device__ __forceinline__ const T* at(int p) const { return src[p]; }
+  };
+  __device__ static __forceinline__ ATable a_table(const T* A, int64_t lda, int64_t rows, const int32_t* idx) {
+    ATable a{A, lda, rows, idx, {}};
+#pragma unroll
+    for (int p = 0; p < A_DIRECT; ++p) {
+      const int r = slot_row(p);
+      a.src[p] = a.row_ptr(r < rows ? r : rows - 1) + slot_chunk(p) * VEC;
+    }
+    return a;
+  }
+
+  template <class AS>
+  __device__ static __forceinline__ void reg_load_a(Regs& R, const AS& as, int64_t k0, int64_t K, bool vec_ok) {
     const int t = threadIdx.x;
     const int c = t & 7;
     const int64_t kk = k0 + c * VEC;
@@ -172,7 +210,7 @@ struct GemmTile {
     for (int p = 0; p < A_LOADS; ++p) {
       const int s = t + THREADS * p;
       const int r = s >> 3;
-      if (s < A_SLOTS && r < rows) R.a[p] = load_chunk<T>(A + (int64_t)r * lda + kk, valid, vec_ok);
+      if (s < A_SLOTS && r < as.rows) R.a[p] = load_chunk<T>(as.row_ptr(r) + kk, valid, vec_ok);
       else R.a[p] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
@@ -271,17 +309,14 @@ struct GemmTile {
   // LDS byte 16*s (row s/8, slot s%8); that slot holds logical chunk (s%8) ^ ((row>>1)&7), so
   // the lane fetches exactly that chunk.  Rows past the problem are clamped to its last row
   // (their products are never stored).
-  __device__ static __forceinline__ void direct_load(char* stage, const T* A, int64_t lda, int64_t rows,
-                                                     const BSource<T>& B, int64_t k0) {
+  template <class AS>
+  __device__ static __forceinline__ void direct_load(char* stage, const AS& as, const BSource<T>& B,
+                                                     int64_t k0) {
     const int t = threadIdx.x;
     const int wbase = t & ~63;
 #pragma unroll
     for (int p = 0; p < A_SLOTS / THREADS; ++p) {
-      const int s = t + THREADS * p;
-      const int r = s >> 3;
-      const int c = (s & 7) ^ ((r >> 1) & 7);
-      const int64_t rr = r < rows ? r : rows - 1;
-      const T* src = A + rr * lda + k0 + c * VEC;
+      const T* src = as.at(p) + k0;
       __builtin_amdgcn_global_load_lds((global_cvoid_t*)src,
                                        (lds_void_t*)(stage + (THREADS * p + wbase) * 16), 16, 0, 0);
     }
@@ -407,8 +442,8 @@ struct GemmTile {
 
   // Full K loop of one tile into acc (zeroed here).  The caller guarantees that no wavefront
   // reads the LDS ring on entry (a barrier separates consecutive tiles).
-  __device__ static __forceinline__ void mainloop(char* smem, Acc (&acc)[FM][FN],
-                                                  const T* A, int64_t lda, int64_t rows, bool a_vec,
+  template <class AS>
+  __device__ static __forceinline__ void mainloop(char* smem, Acc (&acc)[FM][FN], const AS& as, bool a_vec,
                                                   const BSource<T>& B, int64_t K) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -426,7 +461,7 @@ struct GemmTile {
       constexpr int AHEAD = STAGES - 1;  // tiles loaded ahead of the one being computed
 #pragma unroll
       for (int s = 0; s < AHEAD; ++s)
-        if (s < KT) direct_load(smem + s * LDS_STAGE, A, lda, rows, B, (int64_t)s * BK);
+        if (s < KT) direct_load(smem + s * LDS_STAGE, as, B, (int64_t)s * BK);
       if (KT - 1 >= AHEAD - 1) wait_loads<(AHEAD - 1) * LOADS_PER_STAGE>();
       else wait_loads<0>();
       lds_barrier();
@@ -447,7 +482,7 @@ struct GemmTile {
           // reads of its stage), so that stage may now be refilled.
           raw_barrier();
           if (kt + AHEAD < KT)
-            direct_load(smem + nxt * LDS_STAGE, A, lda, rows, B, (kt + AHEAD) * BK);
+            direct_load(smem + nxt * LDS_STAGE, as, B, (kt + AHEAD) * BK);
           load_group(smem + cur * LDS_STAGE, 0, f0);
         }
         mfma_group(acc, f1);
@@ -459,7 +494,7 @@ struct GemmTile {
       constexpr int AHEAD = STAGES - 1;  // tiles in flight beyond the one being computed
 #pragma unroll
       for (int s = 0; s < AHEAD; ++s)
-        if (s < KT) direct_load(smem + s * LDS_STAGE, A, lda, rows, B, (int64_t)s * BK);
+        if (s < KT) direct_load(smem + s * LDS_STAGE, as, B, (int64_t)s * BK);
       int cur = 0;            // stage of tile kt
       int nxt = AHEAD;        // stage of tile kt + AHEAD (== stage of tile kt - 1)
       for (int64_t kt = 0; kt < KT; ++kt) {
@@ -468,7 +503,7 @@ struct GemmTile {
         else wait_loads<0>();
         lds_barrier();  // tile kt visible to all; every wave is done with tile kt - 1
         if (kt + AHEAD < KT)
-          direct_load(smem + nxt * LDS_STAGE, A, lda, rows, B, (kt + AHEAD) * BK);
+          direct_load(smem + nxt * LDS_STAGE, as, B, (kt + AHEAD) * BK);
         compute(smem + cur * LDS_STAGE, acc);
         cur = cur + 1 == STAGES ? 0 : cur + 1;
         nxt = nxt + 1 == STAGES ? 0 : nxt + 1;
@@ -476,7 +511,7 @@ struct GemmTile {
       lds_barrier();
     } else {
       Regs R;
-      reg_load_a(R, A, lda, rows, 0, K, a_vec);
+      reg_load_a(R, as, 0, K, a_vec);
       reg_load_b(R, B, 0, K);
       reg_store(smem, R);
       lds_barrier();
@@ -484,7 +519,7 @@ struct GemmTile {
         const int cur = (int)(kt & 1);
         const bool more = kt + 1 < KT;
         if (more) {
-          reg_load_a(R, A, lda, rows, (kt + 1) * BK, K, a_vec);
+          reg_load_a(R, as, (kt + 1) * BK, K, a_vec);
           reg_load_b(R, B, (kt + 1) * BK, K);
         }
         compute(smem + cur * LDS_STAGE, acc);
@@ -557,8 +592,8 @@ struct GemmTile {
   // Tile k+1 goes into the other stage from P(4k) on (group 0 slots at its load of half step
   // 2k, group 1 slots at its compute of half step 2k-1) and is waited for at the end of
   // P(4k+3).  Same MFMA order per element as every other schedule.
-  __device__ static __forceinline__ void mainloop_pingpong(char* smem, Acc (&acc)[FM][FN],
-                                                           const T* A, int64_t lda, int64_t rows,
+  template <class AS>
+  __device__ static __forceinline__ void mainloop_pingpong(char* smem, Acc (&acc)[FM][FN], const AS& as,
                                                            const BSource<T>& B, int64_t K) {
     static_assert(DIRECT && STAGES == 2 && THREADS == 512 && WGM == 2, "8 waves, 2 stages");
 #pragma unroll
@@ -570,11 +605,11 @@ struct GemmTile {
     const int64_t KT = cdiv(K, BK);
     if (KT == 0) return;
     const bool lag = threadIdx.x >= 256;  // group 1
-    direct_load(smem, A, lda, rows, B, 0);
+    direct_load(smem, as, B, 0);
     wait_loads<0>();
     lds_barrier();  // tile 0 visible
     if (lag) {
-      if (KT > 1) direct_load(smem + LDS_STAGE, A, lda, rows, B, BK);
+      if (KT > 1) direct_load(smem + LDS_STAGE, as, B, BK);
       lds_barrier();  // group 1 starts one phase behind
     }
     for (int64_t kt = 0; kt < KT; ++kt) {
@@ -584,13 +619,13 @@ struct GemmTile {
         Frags f;
         // load phase
         if (!lag && q == 0 && kt + 1 < KT)
-          direct_load(smem + (int)((kt + 1) & 1) * LDS_STAGE, A, lda, rows, B, (kt + 1) * BK);
+          direct_load(smem + (int)((kt + 1) & 1) * LDS_STAGE, as, B, (kt + 1) * BK);
         load_group(st, q, f);
         if (lag && q == 1) wait_loads<0>();  // group 1's slots of tile kt+1
         lds_barrier();
         // compute phase
         if (lag && q == 1 && kt + 2 < KT)
-          direct_load(smem + (int)(kt & 1) * LDS_STAGE, A, lda, rows, B, (kt + 2) * BK);
+          direct_load(smem + (int)(kt & 1) * LDS_STAGE, as, B, (kt + 2) * BK);
         __builtin_amdgcn_s_setprio(1);
         mfma_group(acc, f);
         __builtin_amdgcn_s_setprio(0);

@@ -4,7 +4,8 @@
 //   out[t] = fixed left-to-right sum over the top-k slots of round(y(t, s) * round(w[t,s]))
 // Dense path (biops_moe): every expert for every token, y[e, t] for all (e, t).
 // Sparse path (biops_moe_sparse): the routes r = t*k + s are packed by expert into consecutive
-// rows and each expert multiplies only its own rows (grouped GEMMs).  Every GEMM output row is
+// rows (a row -> token table; the GEMM reads x rows through it) and each expert multiplies only
+// its own rows (grouped GEMMs).  Every GEMM output row is
 // computed by the same fixed MFMA sequence whatever the other rows of its launch are, so the
 // sparse y row of route (t, s) has the bits of the dense y[sel[t,s], t] and both paths give
 // identical outputs.
@@ -139,7 +140,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
 //   plan kernel  counts[c][b] -> routes of chunks before c in bucket b (in place),
 //                off[e]       = first packed row of expert e (experts in index order),
 //                grp1 / grp2  = m-tile tables of the two grouped GEMMs;
-//   gather       row(r) = off[e] + counts[c][e] + rank[r], x[t] copied to packed row row(r).
+//   route rows   row(r) = off[e] + counts[c][e] + rank[r]; row_token[row(r)] = t, the x row the
+//                gate/up GEMM reads for packed row row(r).
 // Packed rows of an expert are therefore its routes in increasing r.
 constexpr int kRankWaves = 4;
 constexpr int kMaxSparseExperts = 2048;
@@ -153,10 +155,9 @@ struct PackArgs {
   int32_t* grp1;       // m-tiles of bm1 rows
   int32_t* grp2;       // m-tiles of bm2 rows
   int32_t* route_row;  // [R], -1 for bucket E
-  const void* x;
-  void* xg;            // [R, D] packed rows
-  int64_t R, k, E, S, chunk, D, sx;
-  int32_t bm1, bm2, elt, vec;
+  int32_t* row_token;  // [R] token of each packed row
+  int64_t R, k, E, S, chunk;
+  int32_t bm1, bm2;
 };
 
 static int64_t route_chunk(int64_t R) {
@@ -292,31 +293,23 @@ __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
 }
 
 // One wavefront per route: its packed row, and its token's row of x copied there.
-__global__ __launch_bounds__(256) void moe_gather_kernel(PackArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+// Packed row of every route (route_row[r], -1 for an invalid expert index) and the token of
+// every packed row (row_token[row] = r / k): the gate/up GEMM reads its A rows through that
+// table, so no copy of x is made.  One thread per route.
+__global__ __launch_bounds__(256) void moe_route_rows_kernel(PackArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r >= a.R) return;
   const int64_t e = a.sel[r];
   const bool ok = e >= 0 && e < a.E;
   int64_t row = -1;
   if (ok) row = (int64_t)a.off[e] + a.counts[(r / a.chunk) * (a.E + 1) + e] + a.rank[r];
-  if (lane == 0) a.route_row[r] = (int32_t)row;
-  if (!ok) return;
-  const int64_t bytes = a.D * a.elt;
-  const char* src = reinterpret_cast<const char*>(a.x) + (r / a.k) * a.sx * a.elt;
-  char* dst = reinterpret_cast<char*>(a.xg) + row * bytes;
-  if (a.vec) {
-    for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16)
-      *reinterpret_cast<u32x4_t*>(dst + o) = *reinterpret_cast<const u32x4_t*>(src + o);
-  } else {
-    for (int64_t o = (int64_t)lane * 2; o < bytes; o += 64 * 2)
-      *reinterpret_cast<uint16_t*>(dst + o) = *reinterpret_cast<const uint16_t*>(src + o);
-  }
+  a.route_row[r] = (int32_t)row;
+  if (ok) a.row_token[row] = (int32_t)(r / a.k);
 }
 
 // Workspace of the sparse path (byte offsets, 256-byte aligned).
 struct SparseLayout {
-  int64_t xg, act, rank, route, counts, off, grp1, grp2, total;
+  int64_t y, act, rank, route, token, counts, off, grp1, grp2, total;
 };
 
 static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int64_t I) {
@@ -326,10 +319,11 @@ static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int6
   const int64_t tiles = cdiv(R, 32) + std::min(E, R);
   SparseLayout L;
   int64_t p = 0;
-  L.xg = p; p += al(R * D * elt);  // gathered x rows; the down projection then writes y here
+  L.y = p; p += al(R * D * elt);  // packed down-projection rows
   L.act = p; p += al(R * I * elt);
   L.rank = p; p += al(R * 4);
   L.route = p; p += al(R * 4);
+  L.token = p; p += al(R * 4);
   L.counts = p; p += al(S * (E + 1) * 4);
   L.off = p; p += al((E + 1) * 4);
   L.grp1 = p; p += al((kGrpHeader + kGrpStride * tiles) * 4);
@@ -475,12 +469,14 @@ extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int6
   int32_t* route_row = reinterpret_cast<int32_t*>(ws + L.route);
 
   if (R > 0) {
-    // Grouped GEMM operands: packed rows, one row group per expert.
-    g.gu.A = ws + L.xg; g.gu.lda = hidden;
+    // Grouped GEMM operands: packed rows, one row group per expert; the gate/up GEMM reads the
+    // x row of each packed row through the row -> token table.
+    int32_t* row_token = reinterpret_cast<int32_t*>(ws + L.token);
+    g.gu.a_rows = row_token;
     g.gu.C = ws + L.act; g.gu.ldc = inter;
     g.gu.grp = reinterpret_cast<const int32_t*>(ws + L.grp1);
     g.dn.A = ws + L.act;
-    g.dn.C = ws + L.xg;
+    g.dn.C = ws + L.y;
     g.dn.grp = reinterpret_cast<const int32_t*>(ws + L.grp2);
     for (BmmArgs* b : {&g.gu, &g.dn}) {
       b->grp_rows = R;
@@ -499,24 +495,21 @@ extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int6
     p.grp1 = reinterpret_cast<int32_t*>(ws + L.grp1);
     p.grp2 = reinterpret_cast<int32_t*>(ws + L.grp2);
     p.route_row = route_row;
-    p.x = x;
-    p.xg = ws + L.xg;
+    p.row_token = row_token;
     p.R = R; p.k = top_k; p.E = experts;
     p.chunk = route_chunk(R);
     p.S = cdiv(R, p.chunk);
-    p.D = hidden; p.sx = sx;
-    p.bm1 = bm1; p.bm2 = bm2; p.elt = elt;
-    p.vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (sx * elt) % 16 == 0 && (hidden * elt) % 16 == 0;
+    p.bm1 = bm1; p.bm2 = bm2;
     const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
     hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)cdiv(p.S, kRankWaves)), dim3(256), hist_bytes, s, p);
     if ((rc = check_launch("moe_rank_kernel")) != BIOPS_OK) return rc;
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
     if ((rc = check_launch("moe_plan_kernel")) != BIOPS_OK) return rc;
-    hipLaunchKernelGGL(moe_gather_kernel, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, p);
-    if ((rc = check_launch("moe_gather_kernel")) != BIOPS_OK) return rc;
+    hipLaunchKernelGGL(moe_route_rows_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, s, p);
+    if ((rc = check_launch("moe_route_rows_kernel")) != BIOPS_OK) return rc;
     if ((rc = launch_bmm(dtype, g.gu, kEpiSwiglu, g.gu_kmajor, s)) != BIOPS_OK) return rc;
     if ((rc = launch_bmm(dtype, g.dn, kEpiPlain, g.dn_kmajor, s)) != BIOPS_OK) return rc;
   }
-  CombineArgs c{ws + L.xg, weights, sel, route_row, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
+  CombineArgs c{ws + L.y, weights, sel, route_row, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
   return launch_combine(dtype, c, s);
 }
