@@ -186,22 +186,22 @@ void bmm_kernel(BmmArgs args) {
   }
 }
 
-// One 32x32 block per workgroup; wavefront 0 stores it straight from the accumulators with the
-// rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
-template <typename T, int AR>
+// One 32 x BC block per workgroup; wavefront 0 stores it straight from the accumulators with
+// the rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
+template <typename T, int AR, int BC>
 __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
-  using S = SkinnyTile<T, AR>;
+  using S = SkinnyTile<T, AR, BC>;
   static_assert(S::THREADS == 512, "launch bounds");
   __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
   const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
   if (t >= (uint32_t)args.total) return;
-  const TileOrigin o = tile_origin(args, t, 32, 32);
+  const TileOrigin o = tile_origin(args, t, 32, BC);
   const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
   const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
                (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
   const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
   const int rows = rows64 < 32 ? (int)rows64 : 32;
-  const int cols = cols64 < 32 ? (int)cols64 : 32;
+  const int cols = cols64 < BC ? (int)cols64 : BC;
   const f32x16_t acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
   if ((threadIdx.x >> 6) != 0) return;
   const int lane = threadIdx.x & 63;
@@ -316,20 +316,33 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   return best;
 }
 
-template <typename T, int AR>
-static int launch_skinny_rows(const BmmArgs& a0, hipStream_t stream) {
+template <typename T, int AR, int BC>
+static int launch_skinny_block(const BmmArgs& a0, hipStream_t stream) {
   BmmArgs a = a0;
   a.tiles_m = cdiv(a.M, 32);
-  a.tiles_n = cdiv(a.N, 32);
+  a.tiles_n = cdiv(a.N, BC);
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
-  hipLaunchKernelGGL((skinny_kernel<T, AR>), dim3((unsigned)a.total), dim3(SkinnyTile<T, AR>::THREADS),
-                     0, stream, a);
+  hipLaunchKernelGGL((skinny_kernel<T, AR, BC>), dim3((unsigned)a.total),
+                     dim3(SkinnyTile<T, AR, BC>::THREADS), 0, stream, a);
   return check_launch("skinny_kernel");
 }
 
-// A rows loaded per stage: the fewest of 8 / 16 / 32 that hold a block's rows.
+// Block width for one row block (M <= 32, no batch): the narrowest of 32 / 16 / 8 columns
+// whose blocks still fit one round on the compute units (N = 2048: 8 columns, 256 blocks).
+// With more row blocks every block re-streams its rows of A, and narrow blocks measured no
+// faster (M = 64, N = 2048, K = 8192: 19.9 us at 16 columns against 19.4 us at 32).
+template <typename T, int AR>
+static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
+  const int64_t cus = device_cus();
+  if (a.nb1 * a.nb2 == 1 && a.M <= 32) {
+    if (cdiv(a.N, 8) <= cus) return launch_skinny_block<T, AR, 8>(a, stream);
+    if (cdiv(a.N, 16) <= cus) return launch_skinny_block<T, AR, 16>(a, stream);
+  }
+  return launch_skinny_block<T, AR, 32>(a, stream);
+}
+
 template <typename T, int BM, int BN, int SB>
 static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   BmmArgs a = a0;
@@ -342,6 +355,7 @@ static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   return check_launch("big_kernel");
 }
 
+// A rows loaded per stage: the fewest of 8 / 16 / 32 that hold a block's rows.
 template <typename T>
 static int launch_skinny(const BmmArgs& a, hipStream_t stream) {
   if (a.M <= 8) return launch_skinny_rows<T, 8>(a, stream);

@@ -1,19 +1,23 @@
-// Skinny GEMM tile for problems with few rows (decode-size linears): one 32x32 block per
+// Skinny GEMM tile for problems with few rows (decode-size linears): one 32 x BC block per
 // workgroup, used when all blocks of a launch fit one round on the compute units.
 //
-// One workgroup owns one 32x32 output block.  Wavefront 0 computes it with exactly the MFMA
-// sequence of GemmTile (K steps of 128 bytes in order; inside a step chunk pairs q = 0..3, lane
-// half h holding chunk 2q+h), so its bits equal those of every other tile entry.  What differs
-// is how operands arrive: eight wavefronts share the 1 KiB global->LDS load instructions of a
-// stage (8 K steps, 1 KiB of every row) round-robin, into a ring of 2-4 stages (up to the
-// 160 KiB of a compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate grows
-// with the bytes per row per stage and with the number of issuing wavefronts (4 KiB per-step
-// stages on one wavefront: ~37 GB/s; 8-step stages on 8 wavefronts: ~2x).  With few rows a
-// block's time is the serial K chain of its accumulator and the weight bytes it streams; the
-// ring keeps the stream ahead of the chain.
+// One workgroup owns one 32 x BC output block (BC = 32, 16 or 8 columns).  Wavefront 0
+// computes it with exactly the MFMA sequence of GemmTile (K steps of 128 bytes in order; inside
+// a step chunk pairs q = 0..3, lane half h holding chunk 2q+h), so its bits equal those of every
+// other tile entry.  What differs is how operands arrive: eight wavefronts share the 1 KiB
+// global->LDS load instructions of a stage (8 K steps, 1 KiB of every row) round-robin, into a
+// ring of 2-4 stages (up to the 160 KiB of a compute unit), and one barrier per stage publishes
+// it.  On MI355X a compute unit's load rate grows with the bytes per row per stage and with the
+// number of issuing wavefronts (4 KiB per-step stages on one wavefront: ~37 GB/s; 8-step
+// stages on 8 wavefronts: ~2x).  With few rows a block's time is the serial K chain of its
+// accumulator and the bytes it streams; the ring keeps the stream ahead of the chain.
 //
 // Only AR A rows are loaded (AR = 8, 16 or 32, the rows a block can hold); MFMA rows past AR
 // read loaded rows again (row r reads row r mod AR) and, like rows past M, are never stored.
+// Likewise only BC B columns are loaded and MFMA column c reads column c mod BC.  An MFMA output
+// element depends on its own A row and B column only, so the BC stored columns carry the bits
+// of a full 32-column block; narrow blocks spread a few-column-block problem (N = 2048: 64
+// blocks of 32) over every compute unit, each streaming BC/32 of the weight bytes.
 //
 // Requirements (checked by the launcher): K-major B, 16-byte aligned A and B rows, K a whole
 // number of 128-byte steps, plain or bias epilogue.
@@ -23,19 +27,25 @@
 
 namespace biops {
 
-template <typename T, int AR>
+template <typename T, int AR, int BC>
 struct SkinnyTile {
   static_assert(AR == 8 || AR == 16 || AR == 32, "A rows per K step");
+  static_assert(BC == 8 || BC == 16 || BC == 32, "B columns per K step");
   static constexpr int WAVES = 8;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
-  static constexpr int IPK = AR / 8 + 4;                  // 1 KiB load instructions per K step
+  static constexpr int IPK = AR / 8 + BC / 8;             // 1 KiB load instructions per K step
   static constexpr int LDS_A = AR * kKBytes;             // A rows of one K step
-  static constexpr int LDS_KSTEP = LDS_A + 32 * kKBytes;  // one K step: A rows, then B columns
+  static constexpr int LDS_KSTEP = LDS_A + BC * kKBytes;  // one K step: A rows, then B columns
   static constexpr int U = 8;                             // K steps per stage (even)
   static constexpr int LDS_STAGE = U * LDS_KSTEP;
-  static constexpr int STAGES = (160 * 1024) / LDS_STAGE;  // 4 / 3 / 2 for AR = 8 / 16 / 32
+  // as deep as 160 KiB allows (4 / 3 / 2 for AR = 8 / 16 / 32 at BC = 32), at most 4 stages:
+  // deeper rings of the narrow blocks measured slower (N = 2048, K = 8192, one row, 8-column
+  // blocks: 13.8 us at 8 stages, 13.3 us at 4, against 12.5 us for the bare chain of 512
+  // dependent MFMAs)
+  static constexpr int STAGES_FIT = (160 * 1024) / LDS_STAGE;
+  static constexpr int STAGES = STAGES_FIT < 4 ? STAGES_FIT : 4;
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
   static constexpr int LOADS = U * IPK / WAVES;           // per wavefront per stage
   static_assert(U * IPK % WAVES == 0, "uniform loads per wavefront");
@@ -63,7 +73,7 @@ struct SkinnyTile {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       f.a[q] = *reinterpret_cast<const u32x4_t*>(kstep + lds_off(ar, 2 * q + lb));
-      f.b[q] = *reinterpret_cast<const u32x4_t*>(kstep + LDS_A + lds_off(lr, 2 * q + lb));
+      f.b[q] = *reinterpret_cast<const u32x4_t*>(kstep + LDS_A + lds_off(lr & (BC - 1), 2 * q + lb));
     }
   }
   __device__ static __forceinline__ void mfma(f32x16_t& acc, const Frags& f) {
@@ -91,7 +101,7 @@ struct SkinnyTile {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // The 32x32 block at (A, B) with `rows` / `cols` valid rows and columns (>= 1) over KT K
+  // The 32 x BC block at (A, B) with `rows` / `cols` valid rows and columns (>= 1) over KT K
   // steps.  Stage s holds K steps s*U .. s*U+U-1 (the last stage may hold fewer).  The U*IPK
   // 1 KiB load instructions of a stage (K step u, part p: A rows 8p..8p+7 or B columns) are
   // dealt round-robin to the 8 wavefronts.  Returns the accumulator in wavefront 0 (other

@@ -205,6 +205,31 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize(("m", "n"), (
+    (1, 2048),     # 8-column skinny blocks (256 of them)
+    (20, 1003),    # 8-column blocks, 3-column last block
+    (32, 4000),    # 16-column blocks (250 of them)
+    (7, 4090),     # 16-column blocks, 10-column last block
+    (128, 2048),   # 32-column blocks
+))
+def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
+    """The skinny entry narrows its blocks to 16 or 8 columns when a problem has few column
+    blocks; the stored columns keep the bits of the table entries."""
+    k = 1024
+    x = gpu(randn(m, k, seed=5200 + m, dtype=dtype))
+    w = gpu(randn(n, k, seed=5201 + n, dtype=dtype))
+    bias = gpu(randn(n, seed=5202, dtype=dtype))
+    skinny = tile_menu.biops_gemm_tile_count() - 2
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = matmul_persistent(x, w.t(), bias)
+    ref_plain = matmul_persistent(x, w.t())
+    assert tile_menu.biops_set_gemm_tile(skinny) == 0
+    assert_bitwise(matmul_persistent(x, w.t(), bias), ref, "skinny entry")
+    assert_bitwise(matmul_persistent(x[m - 1:], w.t(), bias), ref[m - 1:], "skinny entry, last row")
+    assert_bitwise(matmul_persistent(x, w.t()), ref_plain, "skinny entry, no bias")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
 @pytest.mark.parametrize(("m", "k", "n"), (
     (300, 2048, 520),   # N-major direct loads, partial last column tile
     (77, 1024, 256),
