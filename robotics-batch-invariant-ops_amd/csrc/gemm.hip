@@ -37,14 +37,14 @@ BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false)
 BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false)
 #undef BIOPS_CFG
 constexpr int kNumCfg = 12;
-// Entry 12: the skinny tile (gemm_skinny.h), one 32x32 block per workgroup with loader
-// wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
+// Entry 12: the skinny tile (gemm_skinny.h), one 32-row block (32, 16 or 8 columns) per
+// workgroup with loader wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
 // back to the automatic choice.
 constexpr int kSkinnyCfg = kNumCfg;
 // Entry 13: the large-tile schedule (gemm_big.h), 256x256 blocks on four wavefronts (one per
 // SIMD, accumulators in the accumulation registers).  16-bit operands, direct-load conditions
-// and a plain / bias epilogue; elsewhere it falls back to the automatic choice.  It measures
-// within a few percent of entry 0 and is not chosen automatically (forced entries only).
+// and a plain / bias epilogue; elsewhere it falls back to the automatic choice.  Chosen
+// automatically for long K when its tiles fill whole rounds of the compute units.
 constexpr int kBigCfg = kNumCfg + 1;
 constexpr int kMenuSize = kNumCfg + 2;
 
@@ -235,7 +235,7 @@ void big_kernel(BmmArgs args) {
   Tile::mainloop(smem, acc, A, args.lda, rows, B, args.ldb, cols, args.K);
   T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0;
   const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + o.n0 : nullptr;
-  Tile::epilogue(smem, acc, Cp, args.ldc, rows, cols, bias, args.c_vec != 0);
+  Tile::epilogue(acc, Cp, args.ldc, rows, cols, bias);
 }
 
 // -------------------------------------------------------------- tile selection ----
@@ -290,7 +290,8 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   const bool grouped = a.grp != nullptr;
   const int forced = forced_cfg();
   if (forced == kSkinnyCfg && skinny_ok) return forced;
-  const bool big_ok = skinny_ok && dtype != BIOPS_F32;
+  // 32-bit output offsets inside a 256-row tile
+  const bool big_ok = skinny_ok && dtype != BIOPS_F32 && a.ldc < (int64_t(1) << 23);
   if (forced == kBigCfg && big_ok) return forced;
   if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
@@ -313,6 +314,12 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
+  // The four-wave 256x256 entry has the faster K loop but a costlier tile start and end; it wins
+  // for long K when its tiles fill whole rounds of the compute units (MI355X, bf16: 8192^3
+  // 900 us against 959 us, M = 8192 N = 2048 K = 8192 219 us against 230 us, M = 4096 N = 8192
+  // K = 8192 439 us against 458 us; at K = 2048 or with a partial last round it loses).
+  const int64_t big_tiles = batch * cdiv(a.M, 256) * cdiv(a.N, 256);
+  if (big_ok && a.K >= 4096 && big_tiles >= cus && big_tiles % cus == 0) best = kBigCfg;
   return best;
 }
 

@@ -204,6 +204,26 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
         assert_bitwise(matmul_persistent(x[5:6], b, bias), ref[5:6], f"tile entry {cfg}, one row")
 
 
+@pytest.mark.parametrize(("m", "n", "bias"), (
+    (2048, 8192, True),    # 8 x 32 = 256 tiles of 256 x 256: the four-wave large-tile entry
+    (4096, 2048, False),   # 16 x 8 = 128 tiles: a table entry
+))
+def test_long_k_large_tile_choice_keeps_bits(tile_menu, m, n, bias):
+    """At long K the automatic choice may take the four-wave 256x256 entry; rows keep the bits
+    of a table entry and of a one-row call."""
+    k = 4096
+    x = gpu(randn(m, k, seed=5300 + m, dtype=torch.bfloat16))
+    w = gpu(randn(n, k, seed=5301 + n, dtype=torch.bfloat16) * 0.05)
+    b = gpu(randn(n, seed=5302, dtype=torch.bfloat16)) if bias else None
+    tile_menu.biops_set_gemm_tile(-1)
+    auto = matmul_persistent(x, w.t(), b)
+    one = matmul_persistent(x[777:778], w.t(), b)
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = matmul_persistent(x, w.t(), b)
+    assert_bitwise(auto, ref, "automatic entry vs entry 2")
+    assert_bitwise(one, ref[777:778], "one row vs full")
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
 @pytest.mark.parametrize(("m", "n"), (
     (1, 2048),     # 8-column skinny blocks (256 of them)
