@@ -36,7 +36,7 @@ SHAPES = ((8192, 2048, True), (2048, 8192, False))  # (N, K, bias)
 # HBM bytes per launch of the roofline kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
 # (each scaled by what the counter reads for a copy of known size); written next to the
 # rocprofv3 summary that produced it.
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bmm_kernel_bf16_m4096_n8192_k2048_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "big_kernel_bf16_m4096_n8192_k2048_traffic.md")
 
 
 def measured_traffic():
@@ -584,7 +584,7 @@ def main():
         "sweep_tflops_per_m": sweep,
         "roofline": {
             "bound": "mfma",
-            "kernel": f"bmm_kernel<bf16> M={mmax} N={n0} K={k0} +bias",
+            "kernel": f"big_kernel<bf16,256,256> (tile entry 13) M={mmax} N={n0} K={k0} +bias",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",

@@ -44,7 +44,7 @@ constexpr int kSkinnyCfg = kNumCfg;
 // Entry 13: the large-tile schedule (gemm_big.h), 256x256 blocks on four wavefronts (one per
 // SIMD, accumulators in the accumulation registers).  16-bit operands, direct-load conditions
 // and a plain / bias epilogue; elsewhere it falls back to the automatic choice.  Chosen
-// automatically for long K when its tiles fill whole rounds of the compute units.
+// automatically for K >= 2048 when its tiles fill whole rounds of the compute units.
 constexpr int kBigCfg = kNumCfg + 1;
 constexpr int kMenuSize = kNumCfg + 2;
 
@@ -315,11 +315,12 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   }
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
   // The four-wave 256x256 entry has the faster K loop but a costlier tile start and end; it wins
-  // for long K when its tiles fill whole rounds of the compute units (MI355X, bf16: 8192^3
-  // 900 us against 959 us, M = 8192 N = 2048 K = 8192 219 us against 230 us, M = 4096 N = 8192
-  // K = 8192 439 us against 458 us; at K = 2048 or with a partial last round it loses).
+  // when its tiles fill whole rounds of the compute units (MI355X, bf16, against entry 0:
+  // 8192^3 879 us / 956 us, M = 4096 N = 8192 K = 8192 437 / 475 us, M = 8192 N = 2048
+  // K = 8192 221 / 240 us, M = 2048 N = 8192 K = 2048 71.0 / 74.1 us, M = 4096 N = 8192
+  // K = 2048 137.2 / 138.4 us; with a partial last round it loses).
   const int64_t big_tiles = batch * cdiv(a.M, 256) * cdiv(a.N, 256);
-  if (big_ok && a.K >= 4096 && big_tiles >= cus && big_tiles % cus == 0) best = kBigCfg;
+  if (big_ok && a.K >= 2048 && big_tiles >= cus && big_tiles % cus == 0) best = kBigCfg;
   return best;
 }
 

@@ -1,26 +1,25 @@
-// Large-tile GEMM schedule (M >= ~1024): BM x BN block on four wavefronts (2 x 2), each owning
-// a (BM/2) x (BN/2) wave tile whose fp32 accumulators live in the accumulation registers (one
+// Large-tile GEMM schedule (long K): BM x BN block on four wavefronts (2 x 2), each owning a
+// (BM/2) x (BN/2) wave tile whose fp32 accumulators live in the accumulation registers (one
 // wavefront per SIMD, 16 independent 32x32 accumulators at 256 x 256).
 //
 // Same arithmetic as every other tile entry (gemm_core.h): 128-byte K steps in order, chunk
-// pairs q = 0..3 in order inside a step.  A stage of the LDS ring holds SB bytes of K per row
-// (SB = 128: one K step, two stages of 64 KiB at 256 x 256).  Measured on MI355X (bf16,
-// M = 4096, N = 8192, K = 2048): half-step stages (deeper ring, 64-byte requests) and
-// register-staged loads were both slower than this schedule.
+// pairs q = 0..3 in order inside a step.  A stage of the LDS ring holds one K step (SB = 128
+// bytes per row; two stages of 64 KiB at 256 x 256).  Measured on MI355X (bf16, M = 4096,
+// N = 8192, K = 2048): half-step stages (deeper ring, 64-byte requests) and register-staged
+// loads were both slower than this schedule.
 //
-// Stage h (ring slot h % STAGES) holds P = SB / 32 chunk pairs.  Per stage, per wavefront:
-//   group p (p = 0 .. P-1): the MFMAs of pair p, interleaved with the LDS reads of the next
-//   pair (pair p+1, or pair 0 of stage h+1 for the last group);
-//   between groups P-2 and P-1: wait for stage h+1, barrier (publishes h+1; all of stage h
-//   has been read), refill slot h with stage h+STAGES.
+// Stage h (ring slot h % STAGES) holds P = 4 chunk pairs.  Per stage, per wavefront:
+//   group p (p = 0 .. P-2): the MFMAs of pair p, interleaved with the LDS reads of pair p+1;
+//   group P-1: wait for stage h+1 and barrier (publishes h+1; all of stage h has been read),
+//   read pair 0 of stage h+1, then the MFMAs of pair P-1 with the global->LDS loads that
+//   refill slot h with stage h+STAGES interleaved one per MFMA.
 // The compiler waits for all outstanding LDS reads before an MFMA that needs one (the global
 // -> LDS loads make its LDS counter out of order), so each group starts with one wait and its
 // MFMAs only read fragments loaded during the previous group.
 //
-// LDS stage layout: A rows (BM x SB bytes) then B columns (BN x SB bytes).  A 16-byte read
+// LDS stage layout: A rows (BM x 128 bytes) then B columns (BN x 128 bytes).  A 16-byte read
 // serves 16 lanes per clock from a 256-byte window, so 16 consecutive rows reading the same
-// chunk must land in 16 distinct 16-byte slots: chunk c of row r sits at slot c ^ ((r >> 1) & 7)
-// (c ^ ((r >> 2) & 3) for 64-byte rows).
+// chunk must land in 16 distinct 16-byte slots: chunk c of row r sits at slot c ^ ((r >> 1) & 7).
 #pragma once
 
 #include "gemm_core.h"
@@ -30,7 +29,7 @@ namespace biops {
 template <typename T, int BM, int BN, int SB>
 struct BigTile {
   static_assert(sizeof(T) == 2, "16-bit operands");
-  static_assert(SB == 64 || SB == 128, "stage = half or whole K step");
+  static_assert(SB == 128, "whole K step per stage");
   static constexpr int THREADS = 256;
   static constexpr int WM = BM / 2, WN = BN / 2;
   static constexpr int FM = WM / 32, FN = WN / 32;
@@ -57,10 +56,7 @@ struct BigTile {
     u32x4_t b[FN];
   };
 
-  __device__ static __forceinline__ int off(int r, int c) {
-    if constexpr (SB == 128) return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4);
-    else return (r << 6) + ((c ^ ((r >> 2) & 3)) << 4);
-  }
+  __device__ static __forceinline__ int off(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
 
   template <int N>
   __device__ static __forceinline__ void wait_loads() {
@@ -92,17 +88,65 @@ struct BigTile {
       for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], f.a[i], f.b[j]);
   }
 
-  // Interleave the group's MFMAs with its LDS reads (and global->LDS loads, `nv` of them).
-  template <int NV>
+  // Interleave the group's MFMAs with its LDS reads.
   __device__ static __forceinline__ void interleave() {
     constexpr int NM = FM * FN, NR = FM + FN;
     constexpr int MPR = NM / NR > 0 ? NM / NR : 1;  // MFMAs per read
-    constexpr int VPR = (NV + NR - 1) / NR;         // loads per read
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
-      if constexpr (NV > 0) __builtin_amdgcn_sched_group_barrier(0x020, VPR, 0);  // VMEM read
+    }
+  }
+
+  // Direct-load sources of this thread.  Slot s = t + 256p of a stage is row s / 8 of the A
+  // rows (p < A_LOADS) or of the B columns, i.e. row r0 + 32p (r0 = t / 8), holding logical
+  // chunk (t % 8) ^ ((r0 >> 1) & 7) -- the same chunk for every p, 32 being a multiple of 16.
+  // Rows past the valid ones re-load the last valid row (their products are never stored).
+  struct Src {
+    const T* a;
+    const T* b;
+    int64_t lda, ldb;
+    int rows, cols, r0;
+  };
+  __device__ static __forceinline__ Src make_src(const T* A, int64_t lda, int rows, const T* B, int64_t ldb,
+                                                 int cols) {
+    const int t = threadIdx.x;
+    const int r0 = t >> 3;
+    const int c = (t & 7) ^ ((r0 >> 1) & 7);
+    return Src{A + c * VEC, B + c * VEC, lda, ldb, rows, cols, r0};
+  }
+  // Load p of this thread for the stage at K element k into ring slot `slot`.
+  __device__ static __forceinline__ void issue_one(char* smem, const Src& src, int slot, int64_t k, int p) {
+    const int wbase = threadIdx.x & ~63;
+    const T* ptr;
+    if (p < A_LOADS) {
+      const int r = src.r0 + 32 * p;
+      ptr = src.a + (int64_t)(r < src.rows ? r : src.rows - 1) * src.lda;
+    } else {
+      const int r = src.r0 + 32 * (p - A_LOADS);
+      ptr = src.b + (int64_t)(r < src.cols ? r : src.cols - 1) * src.ldb;
+    }
+    __builtin_amdgcn_global_load_lds((global_cvoid_t*)(ptr + k),
+                                     (lds_void_t*)(smem + slot * LDS_STAGE + (THREADS * p + wbase) * 16), 16, 0, 0);
+  }
+  // The MFMAs of one pair with the loads of a stage interleaved, one load after each MFMA.  A
+  // burst of loads ahead of the MFMAs (each load sets M0 and its address first) leaves the MFMA
+  // pipe idle: interleaving measured -4 % at M = 4096, N = 8192, K = 2048 and 8192.
+  __device__ static __forceinline__ void mfmas_loads(Acc (&acc)[FM][FN], const Frags& f, char* smem,
+                                                     const Src& src, int slot, int64_t k) {
+    static_assert(LOADS <= FM * FN, "one load per MFMA at most");
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        Mfma<T>::step(acc[i][j], f.a[i], f.b[j]);
+        if (i * FN + j < LOADS) issue_one(smem, src, slot, k, i * FN + j);
+      }
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
     }
   }
 
@@ -118,35 +162,14 @@ struct BigTile {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     const int64_t H = K / STAGE_ELEMS;  // stages
     if (H == 0) return;
-    const int t = threadIdx.x;
-    const int wbase = t & ~63;
-    // Source of this thread's chunk p of every stage (slot s = t + 256p: row s/CPR, slot s%CPR
-    // holding logical chunk (slot) ^ swizzle(row)).
-    const T* src[LOADS];
+    const Src src = make_src(A, lda, rows, B, ldb, cols);
+    // Stages past the end re-load the last one (into a slot nobody reads again), so every
+    // iteration issues the same loads and the vmcnt waits are constants.
+    auto stage_k = [&](int64_t h) { return (h < H ? h : H - 1) * STAGE_ELEMS; };
 #pragma unroll
-    for (int p = 0; p < LOADS; ++p) {
-      const int s = t + THREADS * p;
-      const int sl = p < A_LOADS ? s : s - BM * CPR;
-      const int r = sl / CPR;
-      const int pos = sl % CPR;
-      const int c = (off(r, pos) >> 4) & (CPR - 1);  // off() is an involution on the slot
-      if (p < A_LOADS) src[p] = A + (int64_t)(r < rows ? r : rows - 1) * lda + c * VEC;
-      else src[p] = B + (int64_t)(r < cols ? r : cols - 1) * ldb + c * VEC;
-    }
-    // Loads of stage h into ring slot `slot`; stages past the end re-load the last one (into a
-    // slot nobody reads again), so every iteration issues the same loads and the vmcnt waits
-    // are constants.
-    auto issue = [&](int slot, int64_t h) {
-      char* st = smem + slot * LDS_STAGE;
-      const int64_t k = (h < H ? h : H - 1) * STAGE_ELEMS;
+    for (int s = 0; s < STAGES; ++s)
 #pragma unroll
-      for (int p = 0; p < LOADS; ++p)
-        __builtin_amdgcn_global_load_lds((global_cvoid_t*)(src[p] + k),
-                                         (lds_void_t*)(st + (THREADS * p + wbase) * 16), 16, 0, 0);
-    };
-
-#pragma unroll
-    for (int s = 0; s < STAGES; ++s) issue(s, s);
+      for (int p = 0; p < LOADS; ++p) issue_one(smem, src, s, stage_k(s), p);
     wait_loads<(STAGES - 1) * LOADS>();  // stage 0 landed
     lds_barrier();
     Frags f[2];
@@ -162,18 +185,17 @@ struct BigTile {
         if (p + 1 < P) {
           read_frags(st, p + 1, next);
           mfmas(acc, use);
-          interleave<0>();
+          interleave();
           __builtin_amdgcn_sched_barrier(0);
         } else {
           // Stage h+1 landed once the STAGES-2 stages issued after it remain in flight.  The
-          // barrier publishes it; every wavefront has read all of stage h, which takes stage
-          // h+STAGES.
+          // barrier publishes it; every wavefront has read all of stage h, whose slot takes
+          // stage h+STAGES.  The next stage's first fragments are read before the loads are
+          // issued (a read after a global->LDS load may not move above it).
           wait_loads<(STAGES - 2) * LOADS>();
           lds_barrier();
-          issue(cur, h + STAGES);
           read_frags(smem + nxt * LDS_STAGE, 0, next);
-          mfmas(acc, use);
-          interleave<LOADS>();
+          mfmas_loads(acc, use, smem, src, cur, stage_k(h + STAGES));
           __builtin_amdgcn_sched_barrier(0);
         }
       }
