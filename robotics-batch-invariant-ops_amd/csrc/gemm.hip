@@ -202,19 +202,11 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
   const int rows = rows64 < 32 ? (int)rows64 : 32;
   const int cols = cols64 < BC ? (int)cols64 : BC;
-  const f32x16_t acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
+  const typename S::Acc acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
   if ((threadIdx.x >> 6) != 0) return;
-  const int lane = threadIdx.x & 63;
-  const int col = lane & 31;
-  if (col >= cols) return;
-  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0 + col;
-  const T* bias = reinterpret_cast<const T*>(args.bias);
-  const float bv = bias ? Num<T>::load(bias + o.n0 + col) : 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    if (row < rows) Num<T>::store(Cp + (int64_t)row * args.ldc, bias ? acc[r] + bv : acc[r]);
-  }
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0;
+  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + o.n0 : nullptr;
+  S::Math::store(acc, Cp, args.ldc, rows, cols, bias);
 }
 
 template <typename T, int BM, int BN, int SB>

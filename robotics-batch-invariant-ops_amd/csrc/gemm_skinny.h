@@ -2,9 +2,8 @@
 // workgroup, used when all blocks of a launch fit one round on the compute units.
 //
 // One workgroup owns one 32 x BC output block (BC = 32, 16 or 8 columns).  Wavefront 0
-// computes it with exactly the MFMA sequence of GemmTile (K steps of 128 bytes in order; inside
-// a step chunk pairs q = 0..3, lane half h holding chunk 2q+h), so its bits equal those of every
-// other tile entry.  What differs is how operands arrive: eight wavefronts share the 1 KiB
+// computes it over K steps of 128 bytes in order, with the arithmetic of SkinnyMath below
+// (bits equal to those of every other tile entry).  What differs is how operands arrive: eight wavefronts share the 1 KiB
 // global->LDS load instructions of a stage (8 K steps, 1 KiB of every row) round-robin, into a
 // ring of 2-4 stages (up to the 160 KiB of a compute unit), and one barrier per stage publishes
 // it.  On MI355X a compute unit's load rate grows with the bytes per row per stage and with the
@@ -26,6 +25,131 @@
 #include "gemm_core.h"
 
 namespace biops {
+
+// Arithmetic of one skinny block.  16-bit types: v_mfma_f32_16x16x32_{bf16,f16} on 16-row x
+// 16-column sub-blocks; quad q' = 0, 1 of a K step feeds chunks 4q'..4q'+3 (lane group g = l/16
+// holding chunk 4q'+g) to one instruction.  On MI355X one such instruction gives the bits of
+// the two v_mfma_f32_32x32x16 of chunk pairs (4q', 4q'+1) and (4q'+2, 4q'+3) that every other
+// tile entry issues: a standalone comparison of both chains over 9.4 M dot products of length
+// 4096 (bf16 and fp16; normal, wide-exponent, cancelling, subnormal, infinite, NaN and
+// overflowing operands) found no differing bit, and the tile-menu tests compare the entries
+// bit for bit.  The 16x16x32 chain is half as long and each link about half as slow, which is
+// what bounds a one-row block with long K.  fp32 keeps the 32x32x2 MFMAs of GemmTile.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+  __device__ static __forceinline__ void step(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16_t> {
+  __device__ static __forceinline__ void step(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), acc, 0, 0, 0);
+  }
+};
+
+template <typename T, int AR, int BC, bool NARROW = (sizeof(T) == 2)>
+struct SkinnyMath;
+
+template <typename T, int AR, int BC>
+struct SkinnyMath<T, AR, BC, true> {
+  static constexpr int RB = AR > 16 ? 2 : 1;  // 16-row sub-blocks
+  static constexpr int CB = BC > 16 ? 2 : 1;  // 16-column sub-blocks
+  struct Acc {
+    f32x4_t c[RB][CB];
+  };
+  struct Frags {
+    u32x4_t a[2][RB];
+    u32x4_t b[2][CB];
+  };
+  __device__ static __forceinline__ void zero(Acc& acc) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) acc.c[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // Lane l reads row / column 16 i + l % 16 (modulo the rows / columns loaded), chunk
+  // 4 q' + l / 16.
+  __device__ static __forceinline__ void load(const char* kstep, int lds_a, Frags& f) {
+    const int lane = threadIdx.x & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        f.a[q][i] = *reinterpret_cast<const u32x4_t*>(kstep + lds_off((16 * i + lr) & (AR - 1), 4 * q + lg));
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        f.b[q][j] = *reinterpret_cast<const u32x4_t*>(kstep + lds_a + lds_off((16 * j + lr) & (BC - 1), 4 * q + lg));
+    }
+  }
+  // MFMA number n of a K step (n = 0 .. COUNT-1, quad-major), so that a caller can place other
+  // instructions after the first one.
+  static constexpr int COUNT = 2 * RB * CB;
+  __device__ static __forceinline__ void one(Acc& acc, const Frags& f, int n) {
+    const int q = n / (RB * CB), i = (n / CB) % RB, j = n % CB;
+    Mfma16<T>::step(acc.c[i][j], f.a[q][i], f.b[q][j]);
+  }
+  // round(acc (+ bias[n])) of this lane's outputs: row 16 i + 4 (l / 16) + r, column
+  // 16 j + l % 16.
+  __device__ static __forceinline__ void store(const Acc& acc, T* C, int64_t ldc, int rows, int cols, const T* bias) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int col = 16 * j + (lane & 15);
+      if (col >= cols) continue;
+      const float bv = bias ? Num<T>::load(bias + col) : 0.f;
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * i + 4 * (lane >> 4) + r;
+          if (row < rows) Num<T>::store(C + (int64_t)row * ldc + col, bias ? acc.c[i][j][r] + bv : acc.c[i][j][r]);
+        }
+    }
+  }
+};
+
+// fp32: the 32x32 block of GemmTile's MFMA sequence (chunk pairs q = 0..3, four 32x32x2 MFMAs
+// each).
+template <typename T, int AR, int BC>
+struct SkinnyMath<T, AR, BC, false> {
+  struct Acc {
+    f32x16_t c;
+  };
+  struct Frags {
+    u32x4_t a[4];
+    u32x4_t b[4];
+  };
+  __device__ static __forceinline__ void zero(Acc& acc) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc.c[r] = 0.f;
+  }
+  __device__ static __forceinline__ void load(const char* kstep, int lds_a, Frags& f) {
+    const int lane = threadIdx.x & 63;
+    const int lr = lane & 31, lb = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f.a[q] = *reinterpret_cast<const u32x4_t*>(kstep + lds_off(lr & (AR - 1), 2 * q + lb));
+      f.b[q] = *reinterpret_cast<const u32x4_t*>(kstep + lds_a + lds_off(lr & (BC - 1), 2 * q + lb));
+    }
+  }
+  static constexpr int COUNT = 4;
+  __device__ static __forceinline__ void one(Acc& acc, const Frags& f, int n) { Mfma<T>::step(acc.c, f.a[n], f.b[n]); }
+  // Row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+  __device__ static __forceinline__ void store(const Acc& acc, T* C, int64_t ldc, int rows, int cols, const T* bias) {
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 31;
+    if (col >= cols) return;
+    const float bv = bias ? Num<T>::load(bias + col) : 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (row < rows) Num<T>::store(C + (int64_t)row * ldc + col, bias ? acc.c[r] + bv : acc.c[r]);
+    }
+  }
+};
 
 template <typename T, int AR, int BC>
 struct SkinnyTile {
@@ -61,24 +185,13 @@ struct SkinnyTile {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 
-  // Fragments of one K step for wavefront 0: a[q], b[q] feed MFMA step q.
-  struct Frags {
-    u32x4_t a[4];
-    u32x4_t b[4];
-  };
-  __device__ static __forceinline__ void load_frags(const char* kstep, Frags& f) {
-    const int lane = threadIdx.x & 63;
-    const int lr = lane & 31, lb = lane >> 5;
-    const int ar = lr & (AR - 1);
+  using Math = SkinnyMath<T, AR, BC>;
+  using Acc = typename Math::Acc;
+  using Frags = typename Math::Frags;
+  __device__ static __forceinline__ void load_frags(const char* kstep, Frags& f) { Math::load(kstep, LDS_A, f); }
+  __device__ static __forceinline__ void mfma(Acc& acc, const Frags& f) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f.a[q] = *reinterpret_cast<const u32x4_t*>(kstep + lds_off(ar, 2 * q + lb));
-      f.b[q] = *reinterpret_cast<const u32x4_t*>(kstep + LDS_A + lds_off(lr & (BC - 1), 2 * q + lb));
-    }
-  }
-  __device__ static __forceinline__ void mfma(f32x16_t& acc, const Frags& f) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) Mfma<T>::step(acc, f.a[q], f.b[q]);
+    for (int n = 0; n < Math::COUNT; ++n) Math::one(acc, f, n);
   }
   // Two consecutive K steps (their fragments read together).
   struct Frags2 {
@@ -87,16 +200,16 @@ struct SkinnyTile {
   // K steps j, j+1 on `f` while the fragments of the two steps at `next` are read into `g`.
   // With an LDS DMA in flight the compiler waits for every outstanding LDS read before an
   // MFMA that needs one, so the reads go out right after the first MFMA and have the other
-  // seven MFMAs (~250 cycles) to land before the next pair's wait.  The scheduling barriers
-  // keep the compiler from sinking each read next to its consumer.
-  __device__ static __forceinline__ void step2(f32x16_t& acc, const Frags2& f, const char* next, Frags2& g) {
-    Mfma<T>::step(acc, f.s[0].a[0], f.s[0].b[0]);
+  // MFMAs of the two steps to land before the next pair's wait.  The scheduling barriers keep
+  // the compiler from sinking each read next to its consumer.
+  __device__ static __forceinline__ void step2(Acc& acc, const Frags2& f, const char* next, Frags2& g) {
+    Math::one(acc, f.s[0], 0);
     __builtin_amdgcn_sched_barrier(0);
     load_frags(next, g.s[0]);
     load_frags(next + LDS_KSTEP, g.s[1]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 1; q < 4; ++q) Mfma<T>::step(acc, f.s[0].a[q], f.s[0].b[q]);
+    for (int n = 1; n < Math::COUNT; ++n) Math::one(acc, f.s[0], n);
     mfma(acc, f.s[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -107,11 +220,10 @@ struct SkinnyTile {
   // dealt round-robin to the 8 wavefronts.  Returns the accumulator in wavefront 0 (other
   // wavefronts return zeros once their last load is issued; the kernel only lets wavefront 0
   // continue).
-  __device__ static __forceinline__ f32x16_t run(char* smem, const T* A, int64_t lda, int rows,
-                                                 const T* B, int64_t ldb, int cols, int64_t KT) {
-    f32x16_t acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  __device__ static __forceinline__ Acc run(char* smem, const T* A, int64_t lda, int rows,
+                                            const T* B, int64_t ldb, int cols, int64_t KT) {
+    Acc acc;
+    Math::zero(acc);
     if (KT == 0) return acc;
     const int w = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;

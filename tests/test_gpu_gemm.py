@@ -204,6 +204,43 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
         assert_bitwise(matmul_persistent(x[5:6], b, bias), ref[5:6], f"tile entry {cfg}, one row")
 
 
+def _adversarial(kind, shape, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    if kind == "wide":  # exponents over +-20 octaves (fp16: +-6)
+        span = 6 if dtype == torch.float16 else 20
+        x = x * torch.pow(2.0, torch.randint(-span, span + 1, shape, generator=g).float())
+    elif kind == "cancel":  # alternating large terms that cancel, small remainders
+        x = torch.where(torch.arange(x.numel()).reshape(shape) % 2 == 0, 64.0 + x, -64.0 + x * 1e-2)
+    elif kind == "tiny":  # products in the subnormal range of fp32
+        x = x * (2.0 ** (-14 if dtype == torch.float16 else -66))
+    elif kind == "inf":
+        x = x.flatten()
+        x[::997] = float("inf")
+        x = x.reshape(shape)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("kind", ("wide", "cancel", "tiny", "inf"))
+@pytest.mark.parametrize("m", (1, 20, 32))
+def test_skinny_entry_bits_on_adversarial_operands(tile_menu, dtype, kind, m):
+    """The skinny entry (16x16x32 MFMAs for 16-bit types) against entry 2 (32x32x16 MFMAs),
+    bit for bit, on operands that stress the accumulation: wide exponents, cancellation,
+    subnormal products and infinities (NaN results compare as equal only when both are NaN)."""
+    k, n = 4096, 1000
+    x = gpu(_adversarial(kind, (m, k), 5400 + m, dtype))
+    w = gpu(_adversarial(kind, (n, k), 5401, dtype))
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = matmul_persistent(x, w.t())
+    skinny = tile_menu.biops_gemm_tile_count() - 2
+    assert tile_menu.biops_set_gemm_tile(skinny) == 0
+    out = matmul_persistent(x, w.t())
+    both_nan = torch.isnan(out) & torch.isnan(ref)
+    assert_bitwise(torch.where(both_nan, torch.zeros_like(out), out),
+                   torch.where(both_nan, torch.zeros_like(ref), ref), f"{kind}, m={m}")
+
+
 @pytest.mark.parametrize(("m", "n", "bias"), (
     (2048, 8192, True),    # 8 x 32 = 256 tiles of 256 x 256: the four-wave large-tile entry
     (4096, 2048, False),   # 16 x 8 = 128 tiles: a table entry
