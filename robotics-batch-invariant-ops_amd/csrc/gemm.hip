@@ -329,17 +329,15 @@ static int launch_skinny_block(const BmmArgs& a0, hipStream_t stream) {
   return check_launch("skinny_kernel");
 }
 
-// Block width for one row block (M <= 32, no batch): the narrowest of 32 / 16 / 8 columns
-// whose blocks still fit one round on the compute units (N = 2048: 8 columns, 256 blocks).
-// With more row blocks every block re-streams its rows of A, and narrow blocks measured no
-// faster (M = 64, N = 2048, K = 8192: 19.9 us at 16 columns against 19.4 us at 32).
+// Block width: the narrowest of 32 / 16 / 8 columns whose blocks still fit one round on the
+// compute units (N = 2048: 8 columns at M <= 32, 16 columns at M = 64).  Measured on MI355X,
+// N = 2048, K = 8192: M = 64 takes 15.5 us at 16 columns against 19.8 us at 32.
 template <typename T, int AR>
 static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
   const int64_t cus = device_cus();
-  if (a.nb1 * a.nb2 == 1 && a.M <= 32) {
-    if (cdiv(a.N, 8) <= cus) return launch_skinny_block<T, AR, 8>(a, stream);
-    if (cdiv(a.N, 16) <= cus) return launch_skinny_block<T, AR, 16>(a, stream);
-  }
+  const int64_t row_blocks = a.nb1 * a.nb2 * cdiv(a.M, 32);
+  if (row_blocks * cdiv(a.N, 8) <= cus) return launch_skinny_block<T, AR, 8>(a, stream);
+  if (row_blocks * cdiv(a.N, 16) <= cus) return launch_skinny_block<T, AR, 16>(a, stream);
   return launch_skinny_block<T, AR, 32>(a, stream);
 }
 
