@@ -204,6 +204,24 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
         assert_bitwise(matmul_persistent(x[5:6], b, bias), ref[5:6], f"tile entry {cfg}, one row")
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("broadcast", (False, True))
+def test_every_tile_entry_gives_identical_bits_bmm(tile_menu, dtype, broadcast):
+    """Batched products (a stride-0 expanded weight included) keep their bits on every entry,
+    the four-wave and skinny entries among them."""
+    a = gpu(randn(3, 300, 2048, seed=5500, dtype=dtype))
+    if broadcast:
+        b = gpu(randn(520, 2048, seed=5501, dtype=dtype)).t().unsqueeze(0).expand(3, -1, -1)
+    else:
+        b = gpu(randn(3, 520, 2048, seed=5501, dtype=dtype)).transpose(1, 2)
+    tile_menu.biops_set_gemm_tile(-1)
+    ref = bmm_persistent(a, b)
+    for cfg in range(tile_menu.biops_gemm_tile_count()):
+        assert tile_menu.biops_set_gemm_tile(cfg) == 0
+        assert_bitwise(bmm_persistent(a, b), ref, f"tile entry {cfg}")
+        assert_bitwise(bmm_persistent(a[1:2, 7:8], b[1:2]), ref[1:2, 7:8], f"tile entry {cfg}, one row")
+
+
 def _adversarial(kind, shape, seed, dtype):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(*shape, generator=g)
