@@ -305,6 +305,12 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
     const double cost = (double)cdiv(tiles, cus) * kCfgBM[c] * kCfgBN[c] / rate;
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
+  // Long K with up to four 32x32 tiles per compute unit: four resident one-wavefront
+  // workgroups keep more of the operand stream in flight than one 64x64 workgroup, despite
+  // twice the bytes (MI355X, M = 512, N = 2048, K = 8192: 39.1 us against 45.8 us; with more
+  // tiles than that the 64x64 entry wins: 54.6 against 78.2 us at M = 1024).
+  if (best == 4 && a.K >= 4096 && !grouped && !swiglu && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= 4 * cus)
+    best = 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
   // The four-wave 256x256 entry has the faster K loop but a costlier tile start and end; it wins
   // when its tiles fill whole rounds of the compute units (MI355X, bf16, against entry 0:
