@@ -7,7 +7,9 @@
 //   * K is consumed in fixed steps of 128 bytes (64 bf16/fp16 or 32 fp32 elements), in order;
 //   * inside a step, 16-byte chunks are paired (2q, 2q+1), q = 0..3 in order, and each pair feeds
 //     one v_mfma_f32_32x32x16_{bf16,f16} (lane half 0 holds chunk 2q, half 1 chunk 2q+1);
-//     fp32 feeds the pair element by element (s = 0..3) to four v_mfma_f32_32x32x2_f32;
+//     fp32 feeds the pair element by element (s = 0..3) to four v_mfma_f32_32x32x2_f32 (the
+//     skinny entry feeds 16-bit chunk quads to v_mfma_f32_16x16x32, which returns the bits of
+//     the two pair steps; gemm_skinny.h);
 //   * out-of-range K is zero in both operands; rows / columns outside the problem never reach
 //     the output;
 //   * there is no split-K: one workgroup owns the whole K loop of its tile.
