@@ -14,27 +14,31 @@ namespace biops {
 // Every entry computes each output element with the same MFMA sequence (see gemm_core.h); the
 // entries differ in block tile, wavefront layout and LDS ring depth only.
 template <int ID> struct Cfg;
-#define BIOPS_CFG(ID, BM_, BN_, WGM_, WGN_, ST_, PERCU_, PP_)                        \
+#define BIOPS_CFG(ID, BM_, BN_, WGM_, WGN_, ST_, PERCU_, PP_, LW_)                   \
   template <> struct Cfg<ID> {                                                    \
     static constexpr int bm = BM_, bn = BN_, wgm = WGM_, wgn = WGN_, stages = ST_;   \
-    static constexpr int threads = 64 * WGM_ * WGN_, per_cu = PERCU_;             \
-    static constexpr int waves_per_eu = (WGM_ * WGN_ * PERCU_ + 3) / 4;           \
+    static constexpr int loaders = LW_;                                           \
+    static constexpr int threads = 64 * (WGM_ * WGN_ + LW_), per_cu = PERCU_;     \
+    static constexpr int waves_per_eu = ((WGM_ * WGN_ + LW_) * PERCU_ + 3) / 4;   \
     static constexpr bool pingpong = PP_;                                         \
     static constexpr bool persist = BM_ * BN_ < 256 * 256;                       \
   };
-//         id   BM   BN  WGM WGN stages  workgroups/CU  ping-pong
-BIOPS_CFG(0, 256, 256, 2, 4, 2, 1, true)
-BIOPS_CFG(1, 256, 128, 2, 2, 3, 1, false)
-BIOPS_CFG(2, 128, 128, 2, 2, 2, 2, false)
-BIOPS_CFG(3, 128, 64, 2, 2, 4, 1, false)
-BIOPS_CFG(4, 64, 64, 2, 2, 4, 2, false)
-BIOPS_CFG(5, 32, 64, 1, 2, 4, 2, false)
-BIOPS_CFG(6, 32, 32, 1, 1, 4, 4, false)
-BIOPS_CFG(7, 256, 256, 2, 4, 2, 1, false)
-BIOPS_CFG(8, 128, 128, 2, 2, 4, 1, false)
-BIOPS_CFG(9, 128, 256, 2, 2, 3, 1, false)
-BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false)
-BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false)
+//         id   BM   BN  WGM WGN stages  workgroups/CU  ping-pong  loader waves
+BIOPS_CFG(0, 256, 256, 2, 4, 2, 1, true, 0)
+BIOPS_CFG(1, 256, 128, 2, 2, 3, 1, false, 0)
+BIOPS_CFG(2, 128, 128, 2, 2, 2, 2, false, 0)
+BIOPS_CFG(3, 128, 64, 2, 2, 4, 1, false, 0)
+BIOPS_CFG(4, 64, 64, 2, 2, 4, 2, false, 0)
+BIOPS_CFG(5, 32, 64, 1, 2, 4, 2, false, 0)
+BIOPS_CFG(6, 32, 32, 1, 1, 4, 4, false, 0)
+// 7: 32x64 tiles (one gate/up pair of 32 columns) on one computing wavefront plus three that only
+// load, into a 12-stage ring: the SwiGLU expert GEMM of few-token MoE calls, a latency-bound
+// weight stream (each wavefront keeps at most 63 loads in flight)
+BIOPS_CFG(7, 32, 64, 1, 1, 12, 1, false, 3)
+BIOPS_CFG(8, 128, 128, 2, 2, 4, 1, false, 0)
+BIOPS_CFG(9, 128, 256, 2, 2, 3, 1, false, 0)
+BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false, 0)
+BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false, 0)
 #undef BIOPS_CFG
 constexpr int kNumCfg = 12;
 // Entry 12: the skinny tile (gemm_skinny.h), one 32-row block (32, 16 or 8 columns) per
@@ -105,7 +109,7 @@ __device__ __forceinline__ TileOrigin tile_origin(const BmmArgs& args, uint32_t 
 template <typename T, int CFG, bool BKM, bool DIRECT, int EPI, bool GRP>
 __device__ __forceinline__ void bmm_tile(const BmmArgs& args, uint32_t t, char* smem) {
   using C = Cfg<CFG>;
-  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
+  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT, C::loaders>;
   constexpr int BM = C::bm, BN = C::bn;
   constexpr int kCols = EPI == kEpiSwiglu ? BN / 2 : BN;
   typename Tile::Acc acc[Tile::FM][Tile::FN];
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(Cfg<CFG>::threads)
 __attribute__((amdgpu_waves_per_eu(Cfg<CFG>::waves_per_eu, Cfg<CFG>::waves_per_eu)))
 void bmm_kernel(BmmArgs args) {
   using C = Cfg<CFG>;
-  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT>;
+  using Tile = GemmTile<T, C::bm, C::bn, C::wgm, C::wgn, (DIRECT ? C::stages : 2), BKM, DIRECT, C::loaders>;
   __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
   const uint32_t G = gridDim.x;
   if constexpr (GRP) {
@@ -235,13 +239,13 @@ void big_kernel(BmmArgs args) {
 // compute unit works through ceil(tiles / CUs) tiles, each costing BM x BN / throughput (two
 // resident workgroups share the unit, so they do not finish sooner), and the entry with the
 // smallest estimate is launched.
-static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 910, 570, 670, 900, 900};
+static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 250, 570, 670, 900, 900};
 // With a 16-bit N-major B on the direct path the fragments come through the transposing LDS
 // reads; measured on MI355X (M = 4096 x N = 8192 / 2048 x K = 2048 / 8192 and 2048 x 1536 x 2048)
 // each entry keeps this share of its K-major rate (small wave tiles lose the most).
-static const double kCfgNmajorShare[kNumCfg] = {0.97, 0.78, 0.86, 0.60, 0.72, 0.60, 0.55, 0.91, 0.73, 0.78, 0.80, 0.83};
-static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 256, 128, 128, 256, 128};
-static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 256, 128, 256, 128, 256};
+static const double kCfgNmajorShare[kNumCfg] = {0.97, 0.78, 0.86, 0.60, 0.72, 0.60, 0.55, 0.60, 0.73, 0.78, 0.80, 0.83};
+static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 32, 128, 128, 256, 128};
+static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 64, 128, 256, 128, 256};
 
 // Forced tile entry (-1: automatic).  Initialised from BIOPS_GEMM_CFG, settable through
 // biops_set_gemm_tile; every entry yields the same bits, so forcing one only changes speed.
@@ -265,16 +269,16 @@ static int forced_cfg() {
 // round re-streams the weights).
 
 // Entries with a kernel for this dtype / epilogue / row mode: no fp32 kernel for 0, 7 and 9;
-// the SwiGLU epilogue needs wave tiles of whole 64-column gate/up pairs and is built for 0, 1
-// and 2; grouped rows are built for a short menu (each entry is a separate kernel).
+// the SwiGLU epilogue needs wave tiles of whole 64-column gate/up pairs and is built for 0, 1,
+// 2 and 7; grouped rows are built for a short menu (each entry is a separate kernel).
 static bool grouped_cfg(int c, bool swiglu) {
-  return swiglu ? (c == 0 || c == 2) : (c == 0 || c == 2 || c == 4 || c == 6 || c == 11);
+  return swiglu ? (c == 0 || c == 2 || c == 7) : (c == 0 || c == 2 || c == 4 || c == 6 || c == 11);
 }
 static bool cfg_ok(int dtype, int c, bool swiglu, bool grouped) {
   if (c < 0 || c >= kNumCfg) return false;
-  if (dtype == BIOPS_F32 && (c == 0 || c == 7 || c == 9)) return false;
+  if (dtype == BIOPS_F32 && (c == 0 || c == 9)) return false;
   if (grouped && !grouped_cfg(c, swiglu)) return false;
-  return !swiglu || c <= 2;
+  return !swiglu || c <= 2 || c == 7;
 }
 
 static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool nmajor16) {
@@ -407,6 +411,7 @@ static int launch_grouped_typed(const BmmArgs& a, bool b_kmajor, bool direct, in
     case 2: return launch_layout<T, 2, EPI, true>(a, b_kmajor, direct, s);
     case 4: if constexpr (kPlain) return launch_layout<T, 4, EPI, true>(a, b_kmajor, direct, s); break;
     case 6: if constexpr (kPlain) return launch_layout<T, 6, EPI, true>(a, b_kmajor, direct, s); break;
+    case 7: if constexpr (!kPlain) return launch_layout<T, 7, EPI, true>(a, b_kmajor, direct, s); break;
     case 11: if constexpr (kPlain) return launch_layout<T, 11, EPI, true>(a, b_kmajor, direct, s); break;
     default: break;
   }
@@ -420,6 +425,7 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 0: if constexpr (sizeof(T) == 2) return launch_layout<T, 0, EPI>(a, b_kmajor, direct, s); break;
       case 1: return launch_layout<T, 1, EPI>(a, b_kmajor, direct, s);
       case 2: return launch_layout<T, 2, EPI>(a, b_kmajor, direct, s);
+      case 7: return launch_layout<T, 7, EPI>(a, b_kmajor, direct, s);
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no SwiGLU kernel for tile config %d", cfg);
@@ -432,7 +438,7 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 4: return launch_layout<T, 4, EPI>(a, b_kmajor, direct, s);
       case 5: return launch_layout<T, 5, EPI>(a, b_kmajor, direct, s);
       case 6: return launch_layout<T, 6, EPI>(a, b_kmajor, direct, s);
-      case 7: if constexpr (sizeof(T) == 2) return launch_layout<T, 7, EPI>(a, b_kmajor, direct, s); break;
+      case 7: return launch_layout<T, 7, EPI>(a, b_kmajor, direct, s);
       case 8: return launch_layout<T, 8, EPI>(a, b_kmajor, direct, s);
       case 9: if constexpr (sizeof(T) == 2) return launch_layout<T, 9, EPI>(a, b_kmajor, direct, s); break;
       case 10: return launch_layout<T, 10, EPI>(a, b_kmajor, direct, s);

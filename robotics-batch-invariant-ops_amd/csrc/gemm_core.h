@@ -124,14 +124,34 @@ typedef __attribute__((address_space(3))) tr16x4_t lds_tr16x4_t;
 __device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_tr16x4_t*)p));
 }
+// The same read as inline assembly, for schedules with global->LDS (DMA) loads in flight: for
+// the builtin the compiler puts a full `s_waitcnt vmcnt(0)` before every transposing read (it
+// cannot rule out that the read aliases a pending DMA write), which drains the whole prefetch
+// ring at every K step.  Those schedules order their reads after the DMA of the same stage by
+// their own waits and barriers.  The compiler does not track the result either: the caller
+// waits with lds_wait_anchor before anything reads it.
+__device__ __forceinline__ u32x2_t lds_read_tr16_asm(const char* p) {
+  u32x2_t r;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
+// Waits for every outstanding LDS operation of the wavefront; x and y count as produced here,
+// so no copy of a lds_read_tr16_asm result can be placed before the wait.
+__device__ __forceinline__ void lds_wait_anchor(u32x2_t& x, u32x2_t& y) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y));
+}
 
-// Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN 32x32 blocks).
-// STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
+// Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN 32x32 blocks);
+// LW further wavefronts only issue loads (more bytes in flight per workgroup: a wavefront keeps at
+// most 63 vector-memory operations outstanding).  STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
 // (16-byte aligned rows, K a multiple of the step; B K-major, or N-major for 16-bit types with
 // whole 8-column chunks); otherwise through registers.
-template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT>
+template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT, int LW = 0>
 struct GemmTile {
-  static constexpr int THREADS = 64 * WGM * WGN;
+  static constexpr int THREADS = 64 * (WGM * WGN + LW);
+  // This wavefront computes (wave-uniform; always true without loader wavefronts).
+  __device__ static __forceinline__ bool computes() { return LW == 0 || (int)(threadIdx.x >> 6) < WGM * WGN; }
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
   static constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -368,18 +388,37 @@ struct GemmTile {
       for (int j = 0; j < FN; ++j)
         b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
     } else {
-      // Lane group g = lane / 16 holds columns 16 (g & 1) .. +15 of the block, K half g >> 1.
-      const int g = lane >> 4, s = lane & 15;
-      const int k = 16 * q + 8 * (g >> 1) + (s >> 2);
-      const int cb = 16 * (g & 1) + 4 * (s & 3);
+      (void)wn;
+      TrHalves h;
+      issue_tr(stage, q, h);
+      finish_tr(h, b);
+    }
+  }
+  // N-major B fragments of MFMA step q through the transposing reads (inline assembly), and the
+  // wait that makes them usable.
+  struct TrHalves {
+    u32x2_t lo[FN], hi[FN];
+  };
+  // Lane group g = lane / 16 holds columns 16 (g & 1) .. +15 of the block, K half g >> 1.
+  __device__ static __forceinline__ void issue_tr(const char* stage, int q, TrHalves& h) {
+    const int lane = threadIdx.x & 63;
+    const int wn = (threadIdx.x >> 6) % WGN;
+    const int g = lane >> 4, s = lane & 15;
+    const int k = 16 * q + 8 * (g >> 1) + (s >> 2);
+    const int cb = 16 * (g & 1) + 4 * (s & 3);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const char* base = stage + LDS_A;
-        const int col = wn * WN + j * 32 + cb;
-        const u32x2_t lo = lds_read_tr16(base + lds_off_n<CPR_N>(k, col));
-        const u32x2_t hi = lds_read_tr16(base + lds_off_n<CPR_N>(k + 4, col));
-        b[j] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-      }
+    for (int j = 0; j < FN; ++j) {
+      const char* base = stage + LDS_A;
+      const int col = wn * WN + j * 32 + cb;
+      h.lo[j] = lds_read_tr16_asm(base + lds_off_n<CPR_N>(k, col));
+      h.hi[j] = lds_read_tr16_asm(base + lds_off_n<CPR_N>(k + 4, col));
+    }
+  }
+  __device__ static __forceinline__ void finish_tr(TrHalves& h, u32x4_t (&b)[FN]) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      lds_wait_anchor(h.lo[j], h.hi[j]);
+      b[j] = u32x4_t{h.lo[j][0], h.lo[j][1], h.hi[j][0], h.hi[j][1]};
     }
   }
 
@@ -389,8 +428,26 @@ struct GemmTile {
     u32x4_t b[2][FN];
   };
   __device__ static __forceinline__ void load_group(const char* stage, int g, Frags& f) {
-    load_frags(stage, 2 * g, f.a[0], f.b[0]);
-    load_frags(stage, 2 * g + 1, f.a[1], f.b[1]);
+    if constexpr (DIRECT && !B_KMAJOR) {
+      // both steps' reads go out before the one wait
+      const int lane = threadIdx.x & 63;
+      const int wm = (threadIdx.x >> 6) / WGN;
+      const int lr = lane & 31, lb = lane >> 5;
+      TrHalves h0, h1;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        f.a[0][i] = *reinterpret_cast<const u32x4_t*>(stage + lds_off(wm * WM + i * 32 + lr, 4 * g + lb));
+      issue_tr(stage, 2 * g, h0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        f.a[1][i] = *reinterpret_cast<const u32x4_t*>(stage + lds_off(wm * WM + i * 32 + lr, 4 * g + 2 + lb));
+      issue_tr(stage, 2 * g + 1, h1);
+      finish_tr(h0, f.b[0]);
+      finish_tr(h1, f.b[1]);
+    } else {
+      load_frags(stage, 2 * g, f.a[0], f.b[0]);
+      load_frags(stage, 2 * g + 1, f.a[1], f.b[1]);
+    }
   }
   __device__ static __forceinline__ void mfma_group(Acc (&acc)[FM][FN], const Frags& f) {
 #pragma unroll
@@ -468,14 +525,17 @@ struct GemmTile {
       else wait_loads<0>();
       lds_barrier();
       Frags f0, f1;
-      load_group(smem, 0, f0);
+      const bool cw = computes();
+      if (cw) load_group(smem, 0, f0);
       int cur = 0;      // stage of tile kt
       int nxt = AHEAD;  // stage of tile kt + AHEAD (== stage of tile kt - 1)
       for (int64_t kt = 0; kt < KT; ++kt) {
         const int cstage = cur;
         cur = cur + 1 == STAGES ? 0 : cur + 1;
-        load_group(smem + cstage * LDS_STAGE, 1, f1);
-        mfma_group(acc, f0);
+        if (cw) {
+          load_group(smem + cstage * LDS_STAGE, 1, f1);
+          mfma_group(acc, f0);
+        }
         if (kt + 1 < KT) {
           // tile kt+1 landed once at most min(AHEAD-2, KT-2-kt) later tiles remain in flight
           if (KT - 2 - kt >= AHEAD - 2) wait_loads<(AHEAD - 2) * LOADS_PER_STAGE>();
@@ -485,9 +545,9 @@ struct GemmTile {
           raw_barrier();
           if (kt + AHEAD < KT)
             direct_load(smem + nxt * LDS_STAGE, as, B, (kt + AHEAD) * BK);
-          load_group(smem + cur * LDS_STAGE, 0, f0);
+          if (cw) load_group(smem + cur * LDS_STAGE, 0, f0);
         }
-        mfma_group(acc, f1);
+        if (cw) mfma_group(acc, f1);
         nxt = nxt + 1 == STAGES ? 0 : nxt + 1;
       }
       lds_barrier();
@@ -506,7 +566,7 @@ struct GemmTile {
         lds_barrier();  // tile kt visible to all; every wave is done with tile kt - 1
         if (kt + AHEAD < KT)
           direct_load(smem + nxt * LDS_STAGE, as, B, (kt + AHEAD) * BK);
-        compute(smem + cur * LDS_STAGE, acc);
+        if (computes()) compute(smem + cur * LDS_STAGE, acc);
         cur = cur + 1 == STAGES ? 0 : cur + 1;
         nxt = nxt + 1 == STAGES ? 0 : nxt + 1;
       }
@@ -524,7 +584,7 @@ struct GemmTile {
           reg_load_a(R, as, (kt + 1) * BK, K, a_vec);
           reg_load_b(R, B, (kt + 1) * BK, K);
         }
-        compute(smem + cur * LDS_STAGE, acc);
+        if (computes()) compute(smem + cur * LDS_STAGE, acc);
         if (more) reg_store(smem + (cur ^ 1) * LDS_STAGE, R);
         lds_barrier();
       }
@@ -546,6 +606,7 @@ struct GemmTile {
     constexpr int PITCH = OUTW * (int)sizeof(T);
     constexpr int SWZ = OUTW / VEC >= 8 ? 7 : OUTW / VEC - 1;  // chunk swizzle stays inside the row
     static_assert(BM * PITCH <= SMEM_BYTES, "epilogue tile must fit the shared memory");
+    if (computes()) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -568,6 +629,7 @@ struct GemmTile {
           Num<T>::store(reinterpret_cast<T*>(smem + row * PITCH) + pos, v);
         }
       }
+    }
     lds_barrier();
     constexpr int CH = OUTW / VEC;
     for (int id = threadIdx.x; id < BM * CH; id += THREADS) {
