@@ -239,10 +239,13 @@ void big_kernel(BmmArgs args) {
 // compute unit works through ceil(tiles / CUs) tiles, each costing BM x BN / throughput (two
 // resident workgroups share the unit, so they do not finish sooner), and the entry with the
 // smallest estimate is launched.
-static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 250, 570, 670, 900, 900};
+static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 180, 570, 670, 900, 900};
 // With a 16-bit N-major B on the direct path the fragments come through the transposing LDS
-// reads; measured on MI355X (M = 4096 x N = 8192 / 2048 x K = 2048 / 8192 and 2048 x 1536 x 2048)
-// each entry keeps this share of its K-major rate (small wave tiles lose the most).
+// reads, and each entry is costed at this share of its K-major rate.  The shares were measured
+// on MI355X (M = 4096 x N = 8192 / 2048 x K = 2048 / 8192 and 2048 x 1536 x 2048) while the
+// compiler still drained the global->LDS loads before those reads; re-measured without that
+// drain the large entries keep 0.94-1.0, but the older shares pick the faster entries for the
+// MoE expert GEMMs (4096 tokens: 553 us per call against 598 us), so they are kept.
 static const double kCfgNmajorShare[kNumCfg] = {0.97, 0.78, 0.86, 0.60, 0.72, 0.60, 0.55, 0.60, 0.73, 0.78, 0.80, 0.83};
 static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 32, 128, 128, 256, 128};
 static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 64, 128, 256, 128, 256};
