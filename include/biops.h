@@ -105,8 +105,9 @@ int biops_gemm_tile_count(void);
  * automatic choice, which is the default; the BIOPS_GEMM_CFG environment variable sets the
  * initial value).  Entries 0, 7 and 9 have no fp32 kernel and fall back to the automatic
  * choice for fp32; entries 12 (one 32x32 block per workgroup with loader wavefronts, for few
- * rows) and 13 (256x256 blocks on four wavefronts, 16-bit types only) need K-major B, 16-byte
- * aligned rows and K a multiple of 128 bytes and fall back to the automatic choice elsewhere.
+ * rows) and 13-19 (blocks of 256x256, 256x128, 128x256, 128x128, 128x64, 64x128 and 64x64 on
+ * four wavefronts, 16-bit types only) need K-major B, 16-byte aligned rows and K a multiple of
+ * 128 bytes and fall back to the automatic choice elsewhere.
  * For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
 int biops_set_gemm_tile(int cfg);
 

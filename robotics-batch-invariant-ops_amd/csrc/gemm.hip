@@ -45,12 +45,17 @@ constexpr int kNumCfg = 12;
 // workgroup with loader wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
 // back to the automatic choice.
 constexpr int kSkinnyCfg = kNumCfg;
-// Entry 13: the large-tile schedule (gemm_big.h), 256x256 blocks on four wavefronts (one per
-// SIMD, accumulators in the accumulation registers).  16-bit operands, direct-load conditions
-// and a plain / bias epilogue; elsewhere it falls back to the automatic choice.  Chosen
-// automatically for K >= 2048 when its tiles fill whole rounds of the compute units.
+// Entries 13-19: the four-wavefront schedule (gemm_big.h), one wavefront per SIMD with the
+// accumulators in the accumulation registers and a ring as deep as the LDS holds, on blocks of
+// 256x256 (entry 13), 256x128, 128x256, 128x128, 128x64, 64x128 and 64x64.  16-bit operands,
+// direct-load conditions and a plain / bias epilogue; elsewhere they fall back to the
+// automatic choice.  Chosen automatically for K >= 2048: entry 13 when its tiles fill whole
+// rounds of the compute units, a smaller block when its tiles fill exactly one round.
 constexpr int kBigCfg = kNumCfg + 1;
-constexpr int kMenuSize = kNumCfg + 2;
+constexpr int kNumBig = 7;
+static const int kBigBM[kNumBig] = {256, 256, 128, 128, 128, 64, 64};
+static const int kBigBN[kNumBig] = {256, 128, 256, 128, 64, 128, 64};
+constexpr int kMenuSize = kBigCfg + kNumBig;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
 // Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
@@ -291,7 +296,7 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   if (forced == kSkinnyCfg && skinny_ok) return forced;
   // 32-bit output offsets inside a 256-row tile
   const bool big_ok = skinny_ok && dtype != BIOPS_F32 && a.ldc < (int64_t(1) << 23);
-  if (forced == kBigCfg && big_ok) return forced;
+  if (forced >= kBigCfg && forced < kMenuSize && big_ok) return forced;
   if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
   const int64_t batch = a.nb1 * a.nb2;
@@ -325,7 +330,17 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // K = 8192 221 / 240 us, M = 2048 N = 8192 K = 2048 71.0 / 74.1 us, M = 4096 N = 8192
   // K = 2048 137.2 / 138.4 us; with a partial last round it loses).
   const int64_t big_tiles = batch * cdiv(a.M, 256) * cdiv(a.N, 256);
-  if (big_ok && a.K >= 2048 && big_tiles >= cus && big_tiles % cus == 0) best = kBigCfg;
+  if (big_ok && a.K >= 2048 && big_tiles >= cus && big_tiles % cus == 0) return kBigCfg;
+  // Its smaller blocks, with rings of 3-10 stages, win against the entries above when their
+  // tiles fill exactly one round.  MI355X, bf16, one box, this entry against the fastest of
+  // entries 0-12 (us): M x N x K = 4096 x 2048 x 8192 120.2 / 127.0 (256x128), 2048 x 2048 x
+  // 8192 71.8 / 80.0 (128x128), 1024 x 2048 x 8192 50.7 / 54.8 (128x64), 512 x 2048 x 8192
+  // 38.9 / 39.2 (64x64), 1024 x 8192 x 2048 36.8 / 37.8, 512 x 8192 x 2048 22.9 / 26.7,
+  // 1024 x 4096 x 4096 38.8 / 45.1.  At 128 x 8192 x 2048 the 64x64 block (13.6) beats the
+  // entry the cost model picks (64x64 on entry 4, 14.2) but not entry 6 (12.5).
+  if (big_ok && a.K >= 2048)
+    for (int i = 1; i < kNumBig; ++i)
+      if (batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]) == cus) return kBigCfg + i;
   return best;
 }
 
@@ -448,6 +463,12 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 11: return launch_layout<T, 11, EPI>(a, b_kmajor, direct, s);
       case kSkinnyCfg: return launch_skinny<T>(a, s);
       case kBigCfg: if constexpr (sizeof(T) == 2) return launch_big<T, 256, 256, 128>(a, s); break;
+      case kBigCfg + 1: if constexpr (sizeof(T) == 2) return launch_big<T, 256, 128, 128>(a, s); break;
+      case kBigCfg + 2: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 256, 128>(a, s); break;
+      case kBigCfg + 3: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 128, 128>(a, s); break;
+      case kBigCfg + 4: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 64, 128>(a, s); break;
+      case kBigCfg + 5: if constexpr (sizeof(T) == 2) return launch_big<T, 64, 128, 128>(a, s); break;
+      case kBigCfg + 6: if constexpr (sizeof(T) == 2) return launch_big<T, 64, 64, 128>(a, s); break;
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);

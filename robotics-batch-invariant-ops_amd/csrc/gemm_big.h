@@ -1,18 +1,21 @@
-// Large-tile GEMM schedule (long K): BM x BN block on four wavefronts (2 x 2), each owning a
+// Four-wavefront GEMM schedule (long K): BM x BN block on four wavefronts (2 x 2), each owning a
 // (BM/2) x (BN/2) wave tile whose fp32 accumulators live in the accumulation registers (one
-// wavefront per SIMD, 16 independent 32x32 accumulators at 256 x 256).
+// wavefront per SIMD, 16 independent 32x32 accumulators at 256 x 256, one at 64 x 64).  Blocks
+// from 256 x 256 down to 64 x 64; the ring takes as many stages as 160 KiB of LDS holds (2 at
+// 256 x 256, 10 at 64 x 64), so one workgroup owns a compute unit.
 //
 // Same arithmetic as every other tile entry (gemm_core.h): 128-byte K steps in order, chunk
 // pairs q = 0..3 in order inside a step.  A stage of the LDS ring holds one K step (SB = 128
-// bytes per row; two stages of 64 KiB at 256 x 256).  Measured on MI355X (bf16, M = 4096,
-// N = 8192, K = 2048): half-step stages (deeper ring, 64-byte requests) and register-staged
-// loads were both slower than this schedule.
+// bytes per row; 64 KiB at 256 x 256).  Measured on MI355X (bf16, M = 4096, N = 8192,
+// K = 2048): half-step stages (deeper ring, 64-byte requests) and register-staged loads were
+// both slower than this schedule.
 //
 // Stage h (ring slot h % STAGES) holds P = 4 chunk pairs.  Per stage, per wavefront:
 //   group p (p = 0 .. P-2): the MFMAs of pair p, interleaved with the LDS reads of pair p+1;
 //   group P-1: wait for stage h+1 and barrier (publishes h+1; all of stage h has been read),
 //   read pair 0 of stage h+1, then the MFMAs of pair P-1 with the global->LDS loads that
-//   refill slot h with stage h+STAGES interleaved one per MFMA.
+//   refill slot h with stage h+STAGES interleaved (one per MFMA at 256 x 256, several per MFMA
+//   in the smaller blocks).
 // The compiler waits for all outstanding LDS reads before an MFMA that needs one (the global
 // -> LDS loads make its LDS counter out of order), so each group starts with one wait and its
 // MFMAs only read fragments loaded during the previous group.
@@ -33,6 +36,7 @@ struct BigTile {
   static constexpr int THREADS = 256;
   static constexpr int WM = BM / 2, WN = BN / 2;
   static constexpr int FM = WM / 32, FN = WN / 32;
+  static constexpr int NM = FM * FN;              // MFMAs per chunk pair
   static constexpr int VEC = 8;
   static constexpr int CPR = SB / 16;             // 16-byte chunks per row of a stage
   static constexpr int P = CPR / 2;               // chunk pairs per stage
@@ -90,7 +94,7 @@ struct BigTile {
 
   // Interleave the group's MFMAs with its LDS reads.
   __device__ static __forceinline__ void interleave() {
-    constexpr int NM = FM * FN, NR = FM + FN;
+    constexpr int NR = FM + FN;
     constexpr int MPR = NM / NR > 0 ? NM / NR : 1;  // MFMAs per read
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
@@ -130,23 +134,30 @@ struct BigTile {
     __builtin_amdgcn_global_load_lds((global_cvoid_t*)(ptr + k),
                                      (lds_void_t*)(smem + slot * LDS_STAGE + (THREADS * p + wbase) * 16), 16, 0, 0);
   }
-  // The MFMAs of one pair with the loads of a stage interleaved, one load after each MFMA.  A
-  // burst of loads ahead of the MFMAs (each load sets M0 and its address first) leaves the MFMA
-  // pipe idle: interleaving measured -4 % at M = 4096, N = 8192, K = 2048 and 8192.
+  // The MFMAs of one pair with the loads of a stage interleaved: MFMA q is followed by loads
+  // [q * LOADS / NM, (q + 1) * LOADS / NM).  A burst of loads ahead of the MFMAs (each load
+  // sets M0 and its address first) leaves the MFMA pipe idle: interleaving measured -4 % at
+  // 256 x 256, M = 4096, N = 8192, K = 2048 and 8192.
   __device__ static __forceinline__ void mfmas_loads(Acc (&acc)[FM][FN], const Frags& f, char* smem,
                                                      const Src& src, int slot, int64_t k) {
-    static_assert(LOADS <= FM * FN, "one load per MFMA at most");
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         Mfma<T>::step(acc[i][j], f.a[i], f.b[j]);
-        if (i * FN + j < LOADS) issue_one(smem, src, slot, k, i * FN + j);
-      }
+        const int q = i * FN + j;
 #pragma unroll
-    for (int i = 0; i < FM * FN; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+        for (int p = q * LOADS / NM; p < (q + 1) * LOADS / NM; ++p) issue_one(smem, src, slot, k, p);
+      }
+    sched_loads<0>();
+  }
+  template <int Q>
+  __device__ static __forceinline__ void sched_loads() {
+    if constexpr (Q < NM) {
+      constexpr int n = (Q + 1) * LOADS / NM - Q * LOADS / NM;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // MFMA
+      if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);  // VMEM
+      sched_loads<Q + 1>();
     }
   }
 
