@@ -319,10 +319,11 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   }
   // Long K with up to four 32x32 tiles per compute unit: four resident one-wavefront
   // workgroups keep more of the operand stream in flight than one 64x64 workgroup, despite
-  // twice the bytes (MI355X, M = 512, N = 2048, K = 8192: 39.1 us against 45.8 us; with more
-  // tiles than that the 64x64 entry wins: 54.6 against 78.2 us at M = 1024).
-  if (best == 4 && a.K >= 4096 && !grouped && !swiglu && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= 4 * cus)
-    best = 6;
+  // twice the bytes (MI355X, M = 512, N = 2048, K = 8192: 39.1 us against 45.8 us; M = 128,
+  // N = 8192, K = 2048: 12.9 against 15.0 us; with more tiles than that the 64x64 entry wins:
+  // 54.6 against 78.2 us at M = 1024, N = 2048, K = 8192).
+  const bool prefer32 = a.K >= 2048 && !grouped && !swiglu && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= 4 * cus;
+  if (best == 4 && prefer32) best = 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
   // The four-wave 256x256 entry has the faster K loop but a costlier tile start and end; it wins
   // when its tiles fill whole rounds of the compute units (MI355X, bf16, against entry 0:
@@ -336,11 +337,13 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // entries 0-12 (us): M x N x K = 4096 x 2048 x 8192 120.2 / 127.0 (256x128), 2048 x 2048 x
   // 8192 71.8 / 80.0 (128x128), 1024 x 2048 x 8192 50.7 / 54.8 (128x64), 512 x 2048 x 8192
   // 38.9 / 39.2 (64x64), 1024 x 8192 x 2048 36.8 / 37.8, 512 x 8192 x 2048 22.9 / 26.7,
-  // 1024 x 4096 x 4096 38.8 / 45.1.  At 128 x 8192 x 2048 the 64x64 block (13.6) beats the
-  // entry the cost model picks (64x64 on entry 4, 14.2) but not entry 6 (12.5).
+  // 1024 x 4096 x 4096 38.8 / 45.1.  Where entry 6 takes four 32x32 tiles per compute unit it
+  // keeps the 64x64 shapes (128 x 8192 x 2048: 12.9 against 13.9 us for the 64x64 block).
   if (big_ok && a.K >= 2048)
-    for (int i = 1; i < kNumBig; ++i)
+    for (int i = 1; i < kNumBig; ++i) {
+      if (kBigBM[i] == 64 && kBigBN[i] == 64 && prefer32) continue;  // see above: entry 6
       if (batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]) == cus) return kBigCfg + i;
+    }
   return best;
 }
 
