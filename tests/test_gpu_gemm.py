@@ -261,22 +261,28 @@ def test_skinny_entry_bits_on_adversarial_operands(tile_menu, dtype, kind, m):
 
 @pytest.mark.parametrize(("m", "n", "bias"), (
     (2048, 8192, True),    # 8 x 32 = 256 tiles of 256 x 256: the four-wave large-tile entry
-    (4096, 2048, False),   # 16 x 8 = 128 tiles: a table entry
+    (4096, 2048, False),   # 256 tiles of 256 x 128: a smaller four-wave block
+    (2048, 2048, True),    # 256 tiles of 128 x 128
+    (1024, 2048, False),   # 256 tiles of 128 x 64
+    (512, 2048, True),     # 32x32 blocks on entry 6 (four per compute unit)
+    (384, 2048, False),    # no whole round for any four-wave block: a table entry
 ))
 def test_long_k_large_tile_choice_keeps_bits(tile_menu, m, n, bias):
-    """At long K the automatic choice may take the four-wave 256x256 entry; rows keep the bits
-    of a table entry and of a one-row call."""
+    """At long K the automatic choice may take a four-wave entry (13-19, on 256 compute
+    units when its blocks fill whole rounds); rows keep the bits of a table entry and of a
+    one-row call."""
     k = 4096
     x = gpu(randn(m, k, seed=5300 + m, dtype=torch.bfloat16))
     w = gpu(randn(n, k, seed=5301 + n, dtype=torch.bfloat16) * 0.05)
     b = gpu(randn(n, seed=5302, dtype=torch.bfloat16)) if bias else None
     tile_menu.biops_set_gemm_tile(-1)
     auto = matmul_persistent(x, w.t(), b)
-    one = matmul_persistent(x[777:778], w.t(), b)
+    row = min(777, m - 1)
+    one = matmul_persistent(x[row:row + 1], w.t(), b)
     assert tile_menu.biops_set_gemm_tile(2) == 0
     ref = matmul_persistent(x, w.t(), b)
     assert_bitwise(auto, ref, "automatic entry vs entry 2")
-    assert_bitwise(one, ref[777:778], "one row vs full")
+    assert_bitwise(one, ref[row:row + 1], "one row vs full")
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
