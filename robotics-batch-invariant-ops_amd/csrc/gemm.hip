@@ -49,12 +49,13 @@ constexpr int kSkinnyCfg = kNumCfg;
 // accumulators in the accumulation registers and a ring as deep as the LDS holds, on blocks of
 // 256x256 (entry 13), 256x128, 128x256, 128x128, 128x64, 64x128 and 64x64.  16-bit operands,
 // direct-load conditions and a plain / bias epilogue; elsewhere they fall back to the
-// automatic choice.  Chosen automatically for K >= 2048: entry 13 when its tiles fill whole
-// rounds of the compute units, a smaller block when its tiles fill exactly one round.
+// automatic choice.  The tile cost model weighs them against entries 0-11 from K = 1024 on.
 constexpr int kBigCfg = kNumCfg + 1;
 constexpr int kNumBig = 7;
 static const int kBigBM[kNumBig] = {256, 256, 128, 128, 128, 64, 64};
 static const int kBigBN[kNumBig] = {256, 128, 256, 128, 64, 128, 64};
+// Throughput of each block in the tile cost model (TFLOP/s-equivalent, as kCfgRate).
+static const double kBigRate[kNumBig] = {1150, 1050, 1050, 850, 700, 700, 480};
 constexpr int kMenuSize = kBigCfg + kNumBig;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
@@ -323,27 +324,23 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // N = 8192, K = 2048: 12.9 against 15.0 us; with more tiles than that the 64x64 entry wins:
   // 54.6 against 78.2 us at M = 1024, N = 2048, K = 8192).
   const bool prefer32 = a.K >= 2048 && !grouped && !swiglu && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= 4 * cus;
+  // The four-wave entries (13-19) join the same cost model from K = 1024 on, at their own
+  // rates.  Measured on MI355X (bf16, one box, against the best of entries 0-12, us):
+  // 3072 x 4096 x 2048 52.3 / 70.1 (256x256, 192 tiles), 2048 x 6144 x 4096 101.8 / 130.6
+  // (256x256), 4096 x 6144 x 4096 184.7 / 200.9 (256x128, three rounds), 4096 x 2048 x 8192
+  // 120.2 / 127.0 (256x128), 2048 x 2048 x 8192 71.8 / 80.0 (128x128), 1024 x 2048 x 8192
+  // 50.7 / 54.8 (128x64), 512 x 8192 x 2048 22.9 / 26.7 (128x128), 2048 x 2048 x 1024
+  // 14.2 / 16.9 (128x128), 1024 x 4096 x 4096 38.8 / 45.1 (128x128).  The 64x64 block loses to
+  // entry 6 where entry 6 fits (128 x 8192 x 2048: 13.6 against 12.5 us).
+  if (big_ok && a.K >= 1024)
+    for (int i = 0; i < kNumBig; ++i) {
+      if (kBigBM[i] == 64 && kBigBN[i] == 64 && prefer32) continue;
+      const int64_t tiles = batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]);
+      const double cost = (double)cdiv(tiles, cus) * kBigBM[i] * kBigBN[i] / kBigRate[i];
+      if (cost < best_cost) { best_cost = cost; best = kBigCfg + i; }
+    }
   if (best == 4 && prefer32) best = 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
-  // The four-wave 256x256 entry has the faster K loop but a costlier tile start and end; it wins
-  // when its tiles fill whole rounds of the compute units (MI355X, bf16, against entry 0:
-  // 8192^3 879 us / 956 us, M = 4096 N = 8192 K = 8192 437 / 475 us, M = 8192 N = 2048
-  // K = 8192 221 / 240 us, M = 2048 N = 8192 K = 2048 71.0 / 74.1 us, M = 4096 N = 8192
-  // K = 2048 137.2 / 138.4 us; with a partial last round it loses).
-  const int64_t big_tiles = batch * cdiv(a.M, 256) * cdiv(a.N, 256);
-  if (big_ok && a.K >= 2048 && big_tiles >= cus && big_tiles % cus == 0) return kBigCfg;
-  // Its smaller blocks, with rings of 3-10 stages, win against the entries above when their
-  // tiles fill exactly one round.  MI355X, bf16, one box, this entry against the fastest of
-  // entries 0-12 (us): M x N x K = 4096 x 2048 x 8192 120.2 / 127.0 (256x128), 2048 x 2048 x
-  // 8192 71.8 / 80.0 (128x128), 1024 x 2048 x 8192 50.7 / 54.8 (128x64), 512 x 2048 x 8192
-  // 38.9 / 39.2 (64x64), 1024 x 8192 x 2048 36.8 / 37.8, 512 x 8192 x 2048 22.9 / 26.7,
-  // 1024 x 4096 x 4096 38.8 / 45.1.  Where entry 6 takes four 32x32 tiles per compute unit it
-  // keeps the 64x64 shapes (128 x 8192 x 2048: 12.9 against 13.9 us for the 64x64 block).
-  if (big_ok && a.K >= 2048)
-    for (int i = 1; i < kNumBig; ++i) {
-      if (kBigBM[i] == 64 && kBigBN[i] == 64 && prefer32) continue;  // see above: entry 6
-      if (batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]) == cus) return kBigCfg + i;
-    }
   return best;
 }
 
