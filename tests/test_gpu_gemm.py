@@ -265,12 +265,12 @@ def test_skinny_entry_bits_on_adversarial_operands(tile_menu, dtype, kind, m):
     (2048, 2048, True),    # 256 tiles of 128 x 128
     (1024, 2048, False),   # 256 tiles of 128 x 64
     (512, 2048, True),     # 32x32 blocks on entry 6 (four per compute unit)
-    (384, 2048, False),    # no whole round for any four-wave block: a table entry
+    (384, 2048, False),    # partial rounds for every block
+    (3072, 4096, True),    # 192 tiles of 256 x 256 (fewer than the compute units)
 ))
 def test_long_k_large_tile_choice_keeps_bits(tile_menu, m, n, bias):
-    """At long K the automatic choice may take a four-wave entry (13-19, on 256 compute
-    units when its blocks fill whole rounds); rows keep the bits of a table entry and of a
-    one-row call."""
+    """At long K the automatic choice may take a four-wave entry (13-19, weighed by the tile
+    cost model); rows keep the bits of a table entry and of a one-row call."""
     k = 4096
     x = gpu(randn(m, k, seed=5300 + m, dtype=torch.bfloat16))
     w = gpu(randn(n, k, seed=5301 + n, dtype=torch.bfloat16) * 0.05)
