@@ -142,41 +142,80 @@ def event_time(fn, iters, stream=None):
     return start.elapsed_time(end) / iters
 
 
-def cpu_baseline(seconds):
-    """The CPU oracle's linear (oracle.linear: fp64 accumulation, one rounding to bf16 -- the
-    restatement of the reference's GEMM the parity tests check against) on a bounded sample of
-    the same workload: M = 256 rows of both configs[1] linears, repeated for ~seconds."""
+def host_description():
+    """CPU model, thread counts and torch's CPU kernel capability of this host."""
     import torch
 
-    import oracle
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            q, period = fh.read().split()[:2]
+            quota = None if q == "max" else round(int(q) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    capability = getattr(getattr(torch.backends, "cpu", None), "get_cpu_capability", lambda: "unknown")()
+    return {"cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0)), "cgroup_cpu_quota": quota,
+            "torch": torch.__version__, "cpu_capability": capability,
+            "onednn": bool(torch.backends.mkldnn.is_available())}
 
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
+
+def cpu_baseline(seconds):
+    """The reference's CPU path on the metric's workload.  With the mode on, the reference
+    registers its overrides on the CUDA dispatch key only (batch_invariant_ops.py:1668-1684),
+    so on CPU tensors ``F.linear`` is stock aten (oneDNN bf16 GEMMs), not linear_batch_invariant
+    (1608-1616).  The same call runs here, under this library's mode (also CUDA-key only), on
+    host bf16 tensors: one pass is both configs[1] linears for every M in 1, 2, 4, ..., 4096 --
+    the GPU step -- repeated for about ``seconds`` on every CPU in this process's affinity set."""
+    import torch
+    import torch.nn.functional as F
+
+    import batch_invariant_ops as bio
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(20)
-    m = 256
-    x = torch.randn(m, 2048, generator=g).to(torch.bfloat16)
-    w1 = (torch.randn(8192, 2048, generator=g) * 0.02).to(torch.bfloat16)
-    b1 = (torch.randn(8192, generator=g) * 0.02).to(torch.bfloat16)
-    w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(torch.bfloat16)
-    h = torch.randn(m, 8192, generator=g).to(torch.bfloat16)
-    oracle.linear(x, w1, b1)
-    oracle.linear(h, w2)
-    flops = 0.0
-    reps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds or reps < 2:
-        oracle.linear(x, w1, b1)
-        oracle.linear(h, w2)
-        flops += 2 * 2.0 * m * 8192 * 2048
-        reps += 1
-    dt = time.perf_counter() - t0
+    operands = []
+    for n, k, has_bias in SHAPES:
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+        b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16) if has_bias else None
+        x = torch.randn(max(M_SWEEP), k, generator=g).to(torch.bfloat16)
+        operands.append((x, w, b))
+
+    def step():
+        for m in M_SWEEP:
+            for x, w, b in operands:
+                F.linear(x[:m], w, b)
+
+    step_flops = sum(2.0 * m * n * k for m in M_SWEEP for n, k, _ in SHAPES)
+    with bio.set_batch_invariant_mode():
+        step()  # warm-up (oneDNN primitive creation)
+        reps = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds or reps < 2:
+            step()
+            reps += 1
+        dt = time.perf_counter() - t0
+    host = host_description()
     return {
-        "value": flops / dt / 1e12,
+        "value": step_flops * reps / dt / 1e12,
         "unit": "TFLOP/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"oracle.linear (torch {torch.__version__} CPU, fp64 accumulate, bf16 rounding) "
-        f"on M=256 rows of both configs[1] linears, {reps} reps in {dt:.1f}s",
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"reference CPU path: F.linear bf16 on host tensors under set_batch_invariant_mode() "
+        f"(stock aten on CPU), the whole M=1..4096 sweep of both configs[1] linears, {reps} passes in "
+        f"{dt:.1f}s on {threads} threads; {host['cpu_model']}, torch {host['torch']}, "
+        f"CPU capability {host['cpu_capability']}, oneDNN {host['onednn']}, "
+        f"cgroup CPU quota {host['cgroup_cpu_quota']}",
+        "ms_per_step": dt * 1e3 / reps,
     }
 
 
@@ -200,9 +239,9 @@ def cpu_config_baselines(seconds=3.0):
     import torch
     import torch.nn.functional as F
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    out = {"cores": cores, "torch": torch.__version__, "kind": "reference CPU path (stock torch ops)"}
+    out = {"cores": cores, "kind": "reference CPU path (stock torch ops)", **host_description()}
     bf = torch.bfloat16
 
     a = torch.linspace(-100, 100, 2048 * 4096).reshape(2048, 4096)

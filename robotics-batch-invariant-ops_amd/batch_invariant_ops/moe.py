@@ -37,8 +37,12 @@ def deterministic_token_choice_moe(
     has the bits of the reference's every-expert evaluation, which ``BIOPS_MOE_DENSE=1``
     selects (also used above 2048 experts).
 
-    Expert indices outside ``[0, E)`` raise ``RuntimeError`` after the kernels ran (the kernels
-    never read out of range); set ``BIOPS_MOE_CHECK_INDICES=0`` to skip that host check.
+    Expert indices outside ``[0, E)`` never make a kernel read out of range: the token's output
+    row is written as zeros.  The call does not wait for the GPU to report them (a host read
+    would synchronise every call, and would fail under stream capture).  With
+    ``BIOPS_MOE_CHECK_INDICES=1`` the call waits for the kernels and raises ``RuntimeError``
+    when an index was out of range.  The reference asserts on the device instead
+    (moe.py:66-73), which ends the process's GPU context.
     """
     del workspace
     return _moe(hidden_states, routing_weights, selected_experts, gate_weight, up_weight, down_weight,
@@ -100,7 +104,8 @@ def _moe(
         ws_bytes = lib.biops_moe_workspace_size(code, token_count, num_experts, hidden_size, intermediate_size)
     # torch's caching allocator returns 512-byte aligned blocks (the sparse path needs 256).
     scratch = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=x.device)
-    bad = torch.zeros(1, dtype=torch.int32, device=x.device)
+    check = nat.env_flag("BIOPS_MOE_CHECK_INDICES", False)
+    bad = torch.zeros(1, dtype=torch.int32, device=x.device) if check else None
     nat.call(
         entry,
         code, token_count, num_experts, hidden_size, intermediate_size, top_k,
@@ -109,10 +114,10 @@ def _moe(
         up.data_ptr(), *up.stride(),
         down.data_ptr(), *down.stride(),
         weights.data_ptr(), code, selected.data_ptr(),
-        out.data_ptr(), bad.data_ptr(),
+        out.data_ptr(), bad.data_ptr() if check else None,
         scratch.data_ptr(), scratch.numel(),
         nat.stream_of(out),
     )
-    if nat.env_flag("BIOPS_MOE_CHECK_INDICES", True) and int(bad.item()) != 0:
+    if check and int(bad.item()) != 0:
         raise RuntimeError("selected_experts contains an expert index outside [0, num_experts)")
     return out

@@ -12,6 +12,7 @@ import torch
 
 import batch_invariant_ops as bio
 from batch_invariant_ops import _native as nat
+from batch_invariant_ops import batch_invariant_ops as bio_ops
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "biops.h")
@@ -260,3 +261,21 @@ def test_missing_gpu_is_a_loud_error():
         pytest.skip("a GPU is present")
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         nat.load(require_gpu=True)
+
+
+def test_get_compute_units_cpu_answer(monkeypatch, capsys):
+    """Without a GPU the reference prints a notice and answers with the torch thread count
+    (batch_invariant_ops.py:249-251)."""
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert bio_ops.get_compute_units() == torch.get_num_threads()
+    assert "Using CPU" in capsys.readouterr().out
+
+
+@pytest.mark.gpu
+def test_get_compute_units_matches_the_device():
+    """On the GPU the answer is the device's compute-unit count (256 on an MI355X)."""
+    props = torch.cuda.get_device_properties(0)
+    assert bio_ops.get_compute_units() == props.multi_processor_count
+    assert lib().biops_compute_units() == props.multi_processor_count
+    if "gfx950" in getattr(props, "gcnArchName", ""):
+        assert bio_ops.get_compute_units() == 256

@@ -200,3 +200,36 @@ def test_varlen_rejects_bad_offsets():
     with pytest.raises(ValueError):
         varlen(q, q[:, :3], q[:, :3], torch.tensor([0, 4], device="cuda"), torch.tensor([0, 3], device="cuda"),
                is_causal=True, causal_type="DontCare")
+
+
+@pytest.mark.parametrize("path", ("fused", "materialized"))
+@pytest.mark.parametrize("case", ("score", "scaled_score", "masked_score"))
+def test_sdpa_rounds_each_bf16_intermediate(case, path, monkeypatch):
+    """The kernels round S, S*scale and S+mask to bf16 like the reference composite: keys whose
+    exact logits differ but round to the same bf16 value get equal weight, so the output is
+    exactly 0.5 (0.67-0.73 without that rounding).  Head size 8 and four keys (two copies of
+    each) so that the fused kernel takes the call too."""
+    if path == "materialized":
+        monkeypatch.setenv("BIOPS_ATTENTION_MATERIALIZE", "1")
+    else:
+        monkeypatch.delenv("BIOPS_ATTENTION_MATERIALIZE", raising=False)
+
+    def t(rows):
+        x = torch.zeros(1, 1, len(rows), 8, dtype=torch.float64)
+        x[0, 0, :, : len(rows[0])] = torch.tensor(rows, dtype=torch.float64)
+        return x.to(torch.bfloat16).cuda()
+
+    v = t([[1.0], [0.0], [1.0], [0.0]])
+    if case == "score":
+        q, k, kw = t([[16.0, 1.0]]), t([[16.0, 1.0], [16.0, 0.0]] * 2), {"scale": 1.0}
+    elif case == "scaled_score":
+        q, k, kw = t([[1.0, 1.0]]), t([[100.0, 100.0], [100.0, 99.0]] * 2), {"scale": 2**-0.5}
+    else:
+        q, k = t([[16.0]]), t([[16.0]] * 4)
+        mask = torch.tensor([[[[1.0, 0.0, 1.0, 0.0]]]]).to(torch.bfloat16).cuda()
+        kw = {"scale": 1.0, "attn_mask": mask}
+    out = sdpa(q, k, v, **kw)
+    assert out[0, 0, 0, 0].item() == 0.5, f"{case} on the {path} path gave {out[0, 0, 0, 0].item()}"
+    ref = oracle.sdpa(q.cpu(), k.cpu(), v.cpu(), **{key: (val.cpu() if isinstance(val, torch.Tensor) else val)
+                                                     for key, val in kw.items()})
+    assert_bitwise(out, ref.cuda(), case)

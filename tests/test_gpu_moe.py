@@ -99,7 +99,7 @@ def test_moe_fused_gate_up_layout():
     assert_close_scaled(out, ref, rel=6 * ULP[torch.bfloat16], abs_scale=6 * ULP[torch.bfloat16] * scale)
 
 
-def test_moe_edge_cases():
+def test_moe_edge_cases(monkeypatch):
     hidden = randn(3, 8, seed=7450).cuda()
     gate = randn(2, 4, 8, seed=7451).cuda()
     down = randn(2, 8, 4, seed=7452).cuda()
@@ -112,6 +112,11 @@ def test_moe_edge_cases():
     with pytest.raises(ValueError):
         moe(hidden, torch.zeros(3, 2, device="cuda"), torch.zeros(3, 1, dtype=torch.int64, device="cuda"),
             gate, gate, down)
+    bad_sel = torch.full((3, 1), 5, dtype=torch.int64, device="cuda")
+    # default: no host synchronisation; the tokens with an invalid expert give zero rows
+    monkeypatch.delenv("BIOPS_MOE_CHECK_INDICES", raising=False)
+    quiet = moe(hidden, torch.ones(3, 1, device="cuda"), bad_sel, gate, gate, down)
+    assert torch.count_nonzero(quiet) == 0
+    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "1")
     with pytest.raises(RuntimeError, match="outside"):
-        moe(hidden, torch.ones(3, 1, device="cuda"), torch.full((3, 1), 5, dtype=torch.int64, device="cuda"),
-            gate, gate, down)
+        moe(hidden, torch.ones(3, 1, device="cuda"), bad_sel, gate, gate, down)

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from model_invariance import compare_outputs, run_investigation
-from model_invariance.harness import first_sample, flatten_outputs, stack_samples, tensor_sha256
+from model_invariance.harness import NOT_REPEATABLE, first_sample, flatten_outputs, stack_samples, tensor_sha256
 
 
 class SyntheticAdapter:
@@ -120,7 +120,7 @@ def test_investigation_stops_a_composition_at_out_of_memory():
 def test_investigation_reports_non_repeatable_model():
     report = run_investigation(SyntheticAdapter(flaky=True), batch_sizes=(1, 2))
     assert not report["repeatability"]["exact"]
-    assert report["failure"] == "same-batch inference is not repeatable"
+    assert report["failure"] == NOT_REPEATABLE
     assert report["composition_results"]["duplicate"] == []
     assert not report["end_to_end_exact"]
 

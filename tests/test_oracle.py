@@ -187,6 +187,33 @@ def test_sdpa_masks_and_scale():
     assert abs(oracle.sdpa(q, k, v, attn_mask=torch.full((1, 1, 1, 2), 5.0)).item() - out.item()) < 1e-6
 
 
+def _bf16(rows):
+    return torch.tensor(rows, dtype=torch.float64).to(BF16)
+
+
+@pytest.mark.parametrize("case", ("score", "scaled_score", "masked_score"))
+def test_sdpa_rounds_each_bf16_intermediate(case):
+    """Each case has two keys whose exact logits differ but whose bf16-rounded logits are equal,
+    with values 1 and 0: with the rounding the output is exactly 0.5; dropping that one rounding
+    gives about 0.67-0.73.
+    score:        q.k = 257 and 256; 257 rounds to 256 (ties to even, spacing 2 above 256).
+    scaled_score: q.k = 200 and 199 (exact); times 1/sqrt(2) = 141.42 and 140.71, both 141.
+    masked_score: q.k = 256 for both keys; key 0 gets +1 from the additive mask, 257 -> 256."""
+    v = _bf16([[[[1.0], [0.0]]]])
+    if case == "score":
+        q, k, kw = _bf16([[[[16.0, 1.0]]]]), _bf16([[[[16.0, 1.0], [16.0, 0.0]]]]), {"scale": 1.0}
+    elif case == "scaled_score":
+        q, k, kw = _bf16([[[[1.0, 1.0]]]]), _bf16([[[[100.0, 100.0], [100.0, 99.0]]]]), {"scale": 2**-0.5}
+    else:
+        q, k = _bf16([[[[16.0, 0.0]]]]), _bf16([[[[16.0, 0.0], [16.0, 0.0]]]])
+        kw = {"scale": 1.0, "attn_mask": _bf16([[[[1.0, 0.0]]]])}
+    assert oracle.sdpa(q, k, v, **kw).item() == 0.5
+    # the same logits without bf16 roundings (fp64 inputs keep every intermediate exact)
+    unrounded = oracle.sdpa(q.double(), k.double(), v.double(), **{
+        key: (val.double() if isinstance(val, torch.Tensor) else val) for key, val in kw.items()})
+    assert 0.6 < unrounded.item() < 0.75
+
+
 def test_varlen_alignment_rules_and_zero_rows():
     # two sequences: (q 2, kv 4) and (q 3, kv 3); Q = 0 -> outputs are means of visible V rows
     q = torch.zeros(1, 6, 1, 4)
