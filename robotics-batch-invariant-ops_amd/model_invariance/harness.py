@@ -168,8 +168,10 @@ def _stats(ref: torch.Tensor, cand: torch.Tensor) -> tuple[int, int, float | Non
     magnitudes = ref.is_floating_point() or ref.is_complex()
     if magnitudes:
         if n:
+            # sum / n rather than mean(): the comparison may run under the batch-invariant
+            # mode, whose mean override has no float64 kernel
             gap = (ref - cand).abs().reshape(-1).double()
-            parts += [gap.max(), gap.mean()]
+            parts += [gap.max(), gap.sum() / n]
         else:
             parts += [torch.zeros((), dtype=torch.float64, device=ne.device)] * 2
     values = torch.stack([p.to(ne.device) for p in parts]).cpu().tolist()
