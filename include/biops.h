@@ -5,7 +5,8 @@
  * void*), launches asynchronously on that stream and returns a status code (BIOPS_OK == 0).
  * On failure biops_last_error() returns a message for the calling thread.  No entry point
  * allocates device memory: scratch space (attention scores, MoE intermediates, work lists) is
- * passed in by the caller, sized by the matching *_workspace_size() query.
+ * passed in by the caller, sized by the matching *_workspace_size() query, except for
+ * biops_moe_sparse_noalloc, whose scratch is a static device array of the library.
  *
  * Batch invariance contract: for every entry point, the arithmetic that produces one output
  * element (the K-reduction order and MFMA instruction of a GEMM, the reduction tree of a row
@@ -295,6 +296,31 @@ int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
                      const void* weights, int w_dtype, const int64_t* sel,
                      void* out, int32_t* bad_index,
                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Size of the static device array behind biops_moe_sparse_noalloc, per GPU (64 MiB). */
+#define BIOPS_MOE_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/* biops_moe_sparse without a workspace argument and without any allocation: the same kernels,
+ * arguments (minus workspace / workspace_bytes) and bit-identical output, with the route tables
+ * and packed matrices in a library-owned static device array of BIOPS_MOE_NOALLOC_SCRATCH_BYTES
+ * on each GPU, held until the process ends.  No hipMalloc / hipFree or other allocating call is
+ * made; the array's device address is looked up once per device (hipGetSymbolAddress, with that
+ * device current).  Sizes whose biops_moe_sparse_workspace_size exceeds the array return
+ * BIOPS_ERR_SIZE before any GPU work (C5 shapes -- hidden 2048, intermediate 768, top-8 -- fit up
+ * to 1485 tokens).  The stream must belong to the current device.  Every call on one GPU uses
+ * the same array: calls that overlap on one GPU (two streams, or two host threads) race and must
+ * be serialised by the caller.  Nothing in the array needs to start at zero: each call writes
+ * every table before reading it.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation). */
+int biops_moe_sparse_noalloc(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,
+                             int64_t top_k,
+                             const void* x, int64_t sx,
+                             const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+                             const void* up, int64_t suE, int64_t suI, int64_t suD,
+                             const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                             const void* weights, int w_dtype, const int64_t* sel,
+                             void* out, int32_t* bad_index, void* stream);
 
 #ifdef __cplusplus
 }

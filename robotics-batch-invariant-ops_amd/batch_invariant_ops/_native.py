@@ -91,7 +91,16 @@ _SIGNATURES = {
         + [_p, _l, _l, _l] * 3
         + [_p, _i, _p, _p, _p, _p, _l, _p],
     ),
+    "biops_moe_sparse_noalloc": (
+        _i,
+        [_i, _l, _l, _l, _l, _l, _p, _l]
+        + [_p, _l, _l, _l] * 3
+        + [_p, _i, _p, _p, _p, _p],
+    ),
 }
+
+# Bytes of the static device array behind biops_moe_sparse_noalloc (BIOPS_MOE_NOALLOC_SCRATCH_BYTES).
+MOE_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 EXPORTED = tuple(_SIGNATURES)
 

@@ -12,6 +12,8 @@
 // No atomics anywhere: route ranks come from wavefront ballots, and every output element is
 // written by exactly one thread.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "gemm.h"
 
@@ -437,23 +439,34 @@ extern "C" int64_t biops_moe_sparse_workspace_size(int dtype, int64_t tokens, in
   return sparse_layout(elt, tokens * top_k, experts, hidden, inter).total;
 }
 
-extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
-                                int64_t inter, int64_t top_k, const void* x, int64_t sx,
-                                const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
-                                const void* up, int64_t suE, int64_t suI, int64_t suD,
-                                const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
-                                const void* weights, int w_dtype, const int64_t* sel, void* out,
-                                int32_t* bad_index, void* workspace, int64_t workspace_bytes,
-                                void* stream) {
+namespace biops {
+
+// Size checks shared by the two sparse entry points (BIOPS_OK, or the failure code with the
+// message set).  Pure host arithmetic: no HIP call.
+static int sparse_sizes_ok(int dtype, int w_dtype, int64_t tokens, int64_t experts, int64_t hidden,
+                           int64_t inter, int64_t top_k) {
   if (!is_float_dtype(dtype) || !is_float_dtype(w_dtype))
     return fail(BIOPS_ERR_DTYPE, "unsupported MoE dtype");
   if (tokens < 0 || experts <= 0 || hidden < 0 || inter < 0 || top_k < 0)
     return fail(BIOPS_ERR_ARG, "invalid MoE sizes");
   if (experts > kMaxSparseExperts)
     return fail(BIOPS_ERR_ARG, "sparse MoE supports up to %d experts", kMaxSparseExperts);
+  if (tokens * top_k >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many routes");
+  return BIOPS_OK;
+}
+
+// The sparse evaluation on a caller-provided workspace (sizes already checked).  Every route
+// table and packed matrix in the workspace is written before it is read within the call, so
+// the workspace needs no clearing and keeps nothing from one call to the next.
+static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,
+                          int64_t top_k, const void* x, int64_t sx, const void* gate, int64_t sgE,
+                          int64_t sgI, int64_t sgD, const void* up, int64_t suE, int64_t suI,
+                          int64_t suD, const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                          const void* weights, int w_dtype, const int64_t* sel, void* out,
+                          int32_t* bad_index, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   if (tokens == 0 || hidden == 0) return BIOPS_OK;
   const int64_t R = tokens * top_k;
-  if (R >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many routes");
   ExpertGemms g;
   int rc = expert_gemms(tokens, experts, hidden, inter, x, sx, gate, sgE, sgI, sgD, up, suE, suI, suD, down,
                         sdE, sdD, sdI, g);
@@ -512,4 +525,78 @@ extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int6
   }
   CombineArgs c{ws + L.y, weights, sel, route_row, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
   return launch_combine(dtype, c, s);
+}
+
+// Scratch of biops_moe_sparse_noalloc: a library-owned device array, one copy on every GPU the
+// library runs on, held until the process ends.  On the host the name `scratch` is only a
+// stand-in for the device symbol; its device address on each GPU comes from
+// hipGetSymbolAddress (noalloc_scratch below) and only that address reaches the kernels.
+static __device__ __align__(256) char scratch[BIOPS_MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mutex;
+}  // namespace
+
+// Device address of `scratch` on the current device, looked up once per device (with that
+// device current) and cached.
+static int noalloc_scratch(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(BIOPS_ERR_HIP, "no current HIP device (or device index >= %d)", kMaxScratchDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return fail(BIOPS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return BIOPS_OK;
+}
+
+}  // namespace biops
+
+extern "C" int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
+                                int64_t inter, int64_t top_k, const void* x, int64_t sx,
+                                const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+                                const void* up, int64_t suE, int64_t suI, int64_t suD,
+                                const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                                const void* weights, int w_dtype, const int64_t* sel, void* out,
+                                int32_t* bad_index, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  const int rc = sparse_sizes_ok(dtype, w_dtype, tokens, experts, hidden, inter, top_k);
+  if (rc != BIOPS_OK) return rc;
+  return moe_sparse_run(dtype, tokens, experts, hidden, inter, top_k, x, sx, gate, sgE, sgI, sgD, up, suE,
+                        suI, suD, down, sdE, sdD, sdI, weights, w_dtype, sel, out, bad_index, workspace,
+                        workspace_bytes, stream);
+}
+
+extern "C" int biops_moe_sparse_noalloc(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
+                                        int64_t inter, int64_t top_k, const void* x, int64_t sx,
+                                        const void* gate, int64_t sgE, int64_t sgI, int64_t sgD,
+                                        const void* up, int64_t suE, int64_t suI, int64_t suD,
+                                        const void* down, int64_t sdE, int64_t sdD, int64_t sdI,
+                                        const void* weights, int w_dtype, const int64_t* sel, void* out,
+                                        int32_t* bad_index, void* stream) {
+  int rc = sparse_sizes_ok(dtype, w_dtype, tokens, experts, hidden, inter, top_k);
+  if (rc != BIOPS_OK) return rc;
+  const int64_t need = sparse_layout(dtype_bytes(dtype), tokens * top_k, experts, hidden, inter).total;
+  if (need > BIOPS_MOE_NOALLOC_SCRATCH_BYTES)
+    return fail(BIOPS_ERR_SIZE,
+                "biops_moe_sparse_noalloc: %lld tokens x top-%lld need %lld bytes of scratch, more than the "
+                "%lld-byte static array; use biops_moe_sparse with a workspace",
+                (long long)tokens, (long long)top_k, (long long)need,
+                (long long)BIOPS_MOE_NOALLOC_SCRATCH_BYTES);
+  if (tokens == 0 || hidden == 0) return BIOPS_OK;
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(&ws)) != BIOPS_OK) return rc;
+  return moe_sparse_run(dtype, tokens, experts, hidden, inter, top_k, x, sx, gate, sgE, sgI, sgD, up, suE,
+                        suI, suD, down, sdE, sdD, sdI, weights, w_dtype, sel, out, bad_index, ws,
+                        BIOPS_MOE_NOALLOC_SCRATCH_BYTES, stream);
 }

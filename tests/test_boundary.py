@@ -279,3 +279,16 @@ def test_get_compute_units_matches_the_device():
     assert lib().biops_compute_units() == props.multi_processor_count
     if "gfx950" in getattr(props, "gcnArchName", ""):
         assert bio_ops.get_compute_units() == 256
+
+
+def test_noalloc_moe_rejects_oversize_before_any_gpu_work():
+    """biops_moe_sparse_noalloc checks its sizes on the host first: 4096 C5 tokens need more
+    than its static array, so it returns BIOPS_ERR_SIZE without touching a device (this runs
+    without a GPU)."""
+    handle = lib()
+    rc = handle.biops_moe_sparse_noalloc(
+        nat.BF16, 4096, 64, 2048, 768, 8, None, 2048, None, 1, 2048, 1, None, 1, 2048, 1,
+        None, 1, 1, 2048, None, nat.BF16, None, None, None, None)
+    assert rc == 5
+    msg = handle.biops_last_error().decode()
+    assert "scratch" in msg and str(nat.MOE_NOALLOC_SCRATCH_BYTES) in msg
