@@ -67,8 +67,18 @@ struct BigTile {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
   }
+  // Through the builtins rather than inline assembly: the compiler then knows that every LDS
+  // read has landed at the barrier.  With the wait hidden in assembly it still counted the
+  // previous group's reads as pending and, once a global->LDS load had been issued after the
+  // barrier, waited for all LDS reads (the next stage's fragments included) before the second
+  // MFMA of the group.  Measured on MI355X (bf16, bitwise-identical outputs), together with the
+  // front-loaded reads of interleave(): 128x64 blocks at M=1024, N=2048, K=8192 53 -> 47 us,
+  // 128x128 at 2048x2048x8192 75 -> 68 us, 256x128 at 4096x2048x8192 -3 %, 256x256 -1.5 %.
   __device__ static __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("" ::: "memory");  // no memory access moves across the barrier (compiler fence)
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
 
   // Chunk pair p of the stage at `stage` for this wavefront's blocks.
@@ -92,15 +102,23 @@ struct BigTile {
       for (int j = 0; j < FN; ++j) Mfma<T>::step(acc[i][j], f.a[i], f.b[j]);
   }
 
-  // Interleave the group's MFMAs with its LDS reads.
+  // Interleave the group's MFMAs with its LDS reads: two reads after each of the group's first
+  // MFMAs, then the remaining MFMAs, so that the reads have most of the group to land before
+  // the next group waits for them (one read per two MFMAs left the last reads two MFMAs before
+  // that wait).
   __device__ static __forceinline__ void interleave() {
     constexpr int NR = FM + FN;
-    constexpr int MPR = NM / NR > 0 ? NM / NR : 1;  // MFMAs per read
+    constexpr int NG = (NR + 1) / 2;  // MFMAs followed by reads; NG <= NM for FM, FN >= 1
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
+    for (int i = 0; i < NR / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
     }
+    if constexpr (NR % 2 != 0) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (NM > NG) __builtin_amdgcn_sched_group_barrier(0x008, NM - NG, 0);
   }
 
   // Direct-load sources of this thread.  Slot s = t + 256p of a stage is row s / 8 of the A

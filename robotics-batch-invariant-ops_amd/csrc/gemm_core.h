@@ -483,13 +483,20 @@ struct GemmTile {
   // Workgroup barrier that orders this thread's LDS reads/writes only: in-flight global loads
   // (the prefetch of later stages) keep running across it, which a fenced __syncthreads()
   // would drain.  Completion of the direct-to-LDS loads is tracked separately (wait_loads).
-  // The "memory" clobber keeps the compiler from moving memory accesses across it.
+  // Written with the builtins so that the compiler knows every LDS read has landed here; with
+  // the wait inside inline assembly it kept the reads pending and, once a global->LDS load was
+  // issued after the barrier, waited for all LDS reads (those just issued included) before the
+  // next MFMA that used an older fragment.
   __device__ static __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("" ::: "memory");  // no memory access moves across the barrier (compiler fence)
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
-  // Barrier that also lets this thread's own LDS reads stay in flight (for reads of a stage
-  // that nobody overwrites before the next barrier).
-  __device__ static __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+  // The barrier between the two MFMA groups of the pipelined schedule.  The reads it could
+  // leave in flight were issued a whole MFMA group earlier, so it waits for them too (see
+  // lds_barrier): the fragments the next group uses then count as landed for the compiler.
+  __device__ static __forceinline__ void raw_barrier() { lds_barrier(); }
 
   // Waits until at most `n` direct loads of this thread are still in flight.
   template <int N>

@@ -181,8 +181,12 @@ struct SkinnyTile {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
   }
+  // Through the builtins, so the compiler knows every LDS read has landed (see GemmTile).
   __device__ static __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("" ::: "memory");  // no memory access moves across the barrier (compiler fence)
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
 
   using Math = SkinnyMath<T, AR, BC>;
