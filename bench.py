@@ -128,18 +128,24 @@ def parse():
     return p.parse_args()
 
 
-def event_time(fn, iters, stream=None):
-    """Average milliseconds per call of fn() measured with HIP events on the launch stream."""
+def event_time(fn, iters, blocks=5):
+    """Milliseconds per call of fn(): HIP events on torch's current stream (the launch stream)
+    around `blocks` blocks of `iters` back-to-back calls; the median block, so that a one-off
+    host stall in one block does not decide the figure."""
     import torch
 
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(iters):
-        fn()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / iters
+    per_call = []
+    for _ in range(blocks):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn()
+        end.record()
+        end.synchronize()
+        per_call.append(start.elapsed_time(end) / iters)
+    per_call.sort()
+    return per_call[len(per_call) // 2]
 
 
 def host_description():

@@ -244,6 +244,42 @@ def bmm_batch_invariant(a, b):
 
 
 # --------------------------------------------------------------- row reductions ----
+_row_fns = {}
+
+
+def _row_fn(name):
+    fn = _row_fns.get(name)
+    if fn is None:
+        fn = _row_fns[name] = nat.function(name)
+    return fn
+
+
+def _last_dim_fast(input, dim) -> int:
+    """Row length when ``input`` is a contiguous CUDA tensor of a kernel dtype reduced over its
+    last dimension with rows to reduce, else 0.  The common RMSNorm / pooling / attention
+    calls take this path straight into the library (per-call host time is what bounds them at
+    model shapes)."""
+    if not input.is_cuda or input.dtype not in nat.DIRECT_DTYPES or not input.is_contiguous():
+        return 0
+    nd = input.dim()
+    if nd == 0 or (dim != -1 and dim != nd - 1):
+        return 0
+    n = input.shape[-1]
+    return n if n > 0 and input.numel() > 0 else 0
+
+
+def _reduce_last_fast(op, input, n, keepdim):
+    """biops_reduce over the last dimension of a contiguous tensor (see _last_dim_fast)."""
+    shape = input.shape
+    out = torch.empty((*shape[:-1], 1) if keepdim else shape[:-1], dtype=input.dtype, device=input.device)
+    code = nat.DIRECT_DTYPES[input.dtype]
+    rc = _row_fn("biops_reduce")(op, code, code, input.numel() // n, n, 1, input.data_ptr(), n, 1, 1,
+                                 out.data_ptr(), nat.stream_of(out))
+    if rc:
+        nat.check(rc, "biops_reduce")
+    return out
+
+
 def _rows_last(input: torch.Tensor, dim: int) -> tuple[torch.Tensor, int]:
     """``input`` with ``dim`` moved last and rows contiguous, plus the normalised dim."""
     dim %= input.ndim
@@ -254,6 +290,15 @@ def _rows_last(input: torch.Tensor, dim: int) -> tuple[torch.Tensor, int]:
 
 
 def _softmax_impl(input, dim, out_dtype, is_log):
+    n = _last_dim_fast(input, dim)
+    if n and out_dtype in nat.DIRECT_DTYPES:
+        out = torch.empty(input.shape, dtype=out_dtype, device=input.device)
+        rc = _row_fn("biops_softmax")(nat.DIRECT_DTYPES[input.dtype], nat.DIRECT_DTYPES[out_dtype],
+                                      input.numel() // n, n, input.data_ptr(), n, out.data_ptr(), n,
+                                      int(is_log), nat.stream_of(out))
+        if rc:
+            nat.check(rc, "biops_softmax")
+        return out
     nat.require_gpu_tensors(input)
     if input.ndim == 0:
         return _softmax_impl(input.reshape(1), 0, out_dtype, is_log).reshape(())
@@ -329,6 +374,10 @@ def mean_dim(
     (M, N, K) with N reduced; integer inputs produce fp32.  Partial sums are fp32 for every
     input dtype.
     """
+    if dtype is None or dtype == input.dtype:
+        n = _last_dim_fast(input, dim)
+        if n:
+            return _reduce_last_fast(nat.REDUCE_MEAN, input, n, keepdim)
     assert input.is_cuda, "Input must be a CUDA tensor"
     assert -input.ndim <= dim < input.ndim, f"Invalid dimension {dim} for tensor with {input.ndim} dimensions"
     if dim < 0:
@@ -363,6 +412,10 @@ def mean_batch_invariant(input, dim, keepdim=False, dtype: torch.dtype | None = 
     (the reference falls back to a stock ``torch.sum`` there).  ``dtype`` is honoured as in
     ``torch.mean`` (the input is cast first).
     """
+    if (dtype is None or dtype == input.dtype) and dim is not None and len(dim) == 1:
+        n = _last_dim_fast(input, dim[0])
+        if n:
+            return _reduce_last_fast(nat.REDUCE_MEAN, input, n, keepdim)
     nat.require_gpu_tensors(input)
     if dtype is not None and input.dtype != dtype:
         input = input.to(dtype)
@@ -404,6 +457,11 @@ def linalg_vector_norm_batch_invariant(
     (batch_invariant_ops.py:1485-1597): a contiguous single-dimension reduction keeps the
     (M, N, K) layout; anything else is permuted to one contiguous row per output.
     """
+    if dtype is None and (ord == 2 or ord == 2.0):
+        d0 = dim if isinstance(dim, int) else (dim[0] if dim is not None and len(dim) == 1 else None)
+        n = _last_dim_fast(input, d0) if d0 is not None else 0
+        if n:
+            return _reduce_last_fast(nat.REDUCE_L2, input, n, keepdim)
     assert input.is_cuda, "input must be a CUDA tensor"
     assert input.is_floating_point(), "only real floating-point inputs are supported"
     assert float(ord) == 2.0, f"only the Euclidean norm is supported, got ord={ord!r}"
