@@ -85,6 +85,30 @@ def profile_kernel(which, iters):
         for _ in range(iters):
             _moe(hidden, wts, sel, gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2),
                  dn.transpose(1, 2), sparse=True)
+    elif which == "varlen":
+        # 32 packed sequences, bottom-right causal (fused varlen kernel)
+        g = torch.Generator().manual_seed(4)
+        lengths = torch.randint(64, 2049, (32,), generator=g)
+        total = int(lengths.sum())
+        q = torch.randn(1, total, 8, 64, generator=g).to(torch.bfloat16).cuda()
+        k = torch.randn(1, total, 2, 64, generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn(1, total, 2, 64, generator=g).to(torch.bfloat16).cuda()
+        cu = torch.zeros(33, dtype=torch.int32)
+        cu[1:] = torch.cumsum(lengths, 0)
+        cu = cu.cuda()
+        for _ in range(iters):
+            bio.varlen_scaled_dot_product_attention_batch_invariant(q, k, v, cu, cu, is_causal=True,
+                                                                   causal_type="BottomRight")
+    elif which == "gemm_mid":
+        # the sweep's lowest-fraction point at M >= 1024: M=1024 on the 8192->2048 linear
+        from batch_invariant_ops import linear_batch_invariant
+
+        g = torch.Generator().manual_seed(20)
+        n, k, _ = SHAPES[1]
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        x = torch.randn(1024, k, generator=g).to(torch.bfloat16).cuda()
+        for _ in range(iters):
+            linear_batch_invariant(x, w)
     elif which == "softmax":
         x = torch.randn(16 * 16 * 1024, 1024, device="cuda").to(torch.bfloat16)
         for _ in range(iters):
@@ -117,12 +141,12 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "copy", "sdpa", "moe", "softmax", "norm"),
+        choices=("gemm", "gemm_mid", "copy", "sdpa", "varlen", "moe", "softmax", "norm"),
         default=None,
-        help="only launch the roofline kernel (gemm), a 512 MiB device copy (copy), configs[2] "
-        "causal attention at B=16 (sdpa), configs[4] MoE at T=4096 (moe), a 262144x1024 bf16 "
-        "softmax (softmax) or a 65536x2048 bf16 row L2 norm (norm) --iters times, for counter "
-        "runs; prints no JSON line",
+        help="only launch the roofline kernel (gemm), the M=1024 8192->2048 linear (gemm_mid), a "
+        "512 MiB device copy (copy), configs[2] causal attention at B=16 (sdpa), configs[3] varlen "
+        "attention (varlen), configs[4] MoE at T=4096 (moe), a 262144x1024 bf16 softmax (softmax) or "
+        "a 65536x2048 bf16 row L2 norm (norm) --iters times, for counter runs; prints no JSON line",
     )
     p.add_argument("--iters", type=int, default=10)
     return p.parse_args()
