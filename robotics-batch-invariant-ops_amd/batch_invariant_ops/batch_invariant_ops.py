@@ -644,14 +644,24 @@ def scaled_dot_product_attention_batch_invariant(
     return out.reshape(*leading, Lq, Dv)
 
 
-def _varlen_plan(q_offsets, kv_offsets, heads, value_dim, dtype):
+def _offsets_on_host(cu_q, cu_kv):
+    """Both offset lists as host int64 arrays: one blocking device-to-host copy (the reference
+    synchronises here too, batch_invariant_ops.py:1264-1265), shared when the query and key
+    offsets are the same tensor, as in self-attention over a packed batch."""
     import numpy as np
 
-    nseq = len(q_offsets) - 1
+    host_q = np.ascontiguousarray(cu_q.detach().cpu().numpy(), dtype=np.int64)
+    if cu_kv is cu_q:
+        return host_q, host_q
+    return host_q, np.ascontiguousarray(cu_kv.detach().cpu().numpy(), dtype=np.int64)
+
+
+def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype):
+    import numpy as np
+
+    nseq = len(cu_q) - 1
     lib = nat.load()
     plan = np.zeros(lib.biops_varlen_plan_len(nseq), dtype=np.int64)
-    cu_q = np.asarray(q_offsets, dtype=np.int64)
-    cu_kv = np.asarray(kv_offsets, dtype=np.int64)
     ws_bytes = lib.biops_varlen_plan(
         nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype), plan.ctypes.data
     )
@@ -702,45 +712,50 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     if query.dtype not in _FLOAT_DTYPES:
         raise ValueError(f"unsupported varlen attention dtype: {query.dtype}")
 
-    q_offsets = [int(x) for x in cumulative_seqlen_q.detach().cpu().tolist()]
-    kv_offsets = [int(x) for x in cumulative_seqlen_kv.detach().cpu().tolist()]
-    if not q_offsets or q_offsets[0] != 0 or kv_offsets[0] != 0:
+    cu_q, cu_kv = _offsets_on_host(cumulative_seqlen_q, cumulative_seqlen_kv)
+    if cu_q.size == 0 or cu_q[0] != 0 or cu_kv[0] != 0:
         raise ValueError("cumulative sequence lengths must start at zero")
-    if q_offsets[-1] > query.shape[1] or kv_offsets[-1] > key.shape[1]:
+    if cu_q[-1] > query.shape[1] or cu_kv[-1] > key.shape[1]:
         raise ValueError("cumulative sequence lengths exceed packed tensor size")
     nat.require_gpu_tensors(query, key, value)
 
     causal_name = getattr(causal_type, "name", None)
     if causal_name is None and causal_type is not None:
         causal_name = str(causal_type).rsplit(".", 1)[-1]
-    for q0, q1, k0, k1 in zip(q_offsets[:-1], q_offsets[1:], kv_offsets[:-1], kv_offsets[1:]):
-        q_len, kv_len = q1 - q0, k1 - k0
-        if q_len < 0 or kv_len < 0:
-            raise ValueError("cumulative sequence lengths must be nondecreasing")
-        if is_causal and q_len > 0 and kv_len > 0 and q_len != kv_len:
-            if causal_name not in {"BottomRight", "TopLeft", None}:
-                raise ValueError(f"causal type {causal_name!r} requires equal query and KV lengths")
+    q_lens, kv_lens = cu_q[1:] - cu_q[:-1], cu_kv[1:] - cu_kv[:-1]
+    if (q_lens < 0).any() or (kv_lens < 0).any():
+        raise ValueError("cumulative sequence lengths must be nondecreasing")
+    if is_causal and causal_name not in {"BottomRight", "TopLeft", None}:
+        if ((q_lens > 0) & (kv_lens > 0) & (q_lens != kv_lens)).any():
+            raise ValueError(f"causal type {causal_name!r} requires equal query and KV lengths")
 
     heads, kv_heads = query.shape[2], key.shape[2]
     head_dim, value_dim = query.shape[3], value.shape[3]
-    output = torch.zeros((1, query.shape[1], heads, value_dim), dtype=value.dtype, device=value.device)
-    if len(q_offsets) <= 1 or output.numel() == 0:
-        return output
-    plan, ws_bytes = _varlen_plan(q_offsets, kv_offsets, heads, value_dim, query.dtype)
+    out_shape = (1, query.shape[1], heads, value_dim)
+    if cu_q.size <= 1 or math.prod(out_shape) == 0:
+        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
+    plan, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype)
     if plan[0] == 0:
-        return output
+        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
 
     def tokens_heads(x):
         return x if x.stride(3) == 1 or x.shape[3] <= 1 else x.contiguous()
 
     q, k, v = tokens_heads(query), tokens_heads(key), tokens_heads(value)
-    dplan = torch.from_numpy(plan).to(query.device)
+    fused = _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v, varlen=True)
+    # The fused kernel writes every row of every sequence it computes; rows outside the
+    # sequences, or of a sequence with an empty key range, must read as zero.
+    every_row_written = fused and cu_q[-1] == query.shape[1] and bool(((kv_lens > 0) | (q_lens == 0)).all())
+    output = (torch.empty if every_row_written else torch.zeros)(out_shape, dtype=value.dtype, device=value.device)
+    # the work list goes up from pinned memory without blocking the host (torch's pinned-memory
+    # cache keeps the staging block until the copy has run)
+    dplan = torch.from_numpy(plan).pin_memory().to(query.device, non_blocking=True)
     if is_causal:
         causal = nat.CAUSAL_BOTTOM_RIGHT if causal_name == "BottomRight" else nat.CAUSAL_TOP_LEFT
     else:
         causal = nat.CAUSAL_NONE
     scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
-    if _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v, varlen=True):
+    if fused:
         nat.call(
             "biops_varlen_sdpa_fused",
             nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
