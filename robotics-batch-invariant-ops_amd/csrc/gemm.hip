@@ -54,8 +54,14 @@ constexpr int kBigCfg = kNumCfg + 1;
 constexpr int kNumBig = 7;
 static const int kBigBM[kNumBig] = {256, 256, 128, 128, 128, 64, 64};
 static const int kBigBN[kNumBig] = {256, 128, 256, 128, 64, 128, 64};
-// Throughput of each block in the tile cost model (TFLOP/s-equivalent, as kCfgRate).
-static const double kBigRate[kNumBig] = {1150, 1050, 1050, 850, 700, 700, 480};
+// Throughput of each block in the tile cost model (TFLOP/s-equivalent, as kCfgRate).  The
+// 64x128 block is rated above the 128x64 one: measured on MI355X it was 3-7 % faster on every
+// shape where both fill the same rounds (M=1024, N=2048, K=8192: 47.4 against 51.3 us; M=256,
+// N=8192, K=2048: 15.7 against 16.4 us).  The 64x64 block (rate unused) stays out of the
+// automatic choice: entry 6 (four 32x32 workgroups per unit) or entry 4 matched or beat it on
+// every shape measured (M=64..512 at N=8192, K=2048 and N=2048, K=8192).
+static const double kBigRate[kNumBig] = {1150, 1050, 1050, 850, 700, 720, 480};
+constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weighs
 constexpr int kMenuSize = kBigCfg + kNumBig;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
@@ -330,11 +336,9 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // (256x256), 4096 x 6144 x 4096 184.7 / 200.9 (256x128, three rounds), 4096 x 2048 x 8192
   // 120.2 / 127.0 (256x128), 2048 x 2048 x 8192 71.8 / 80.0 (128x128), 1024 x 2048 x 8192
   // 50.7 / 54.8 (128x64), 512 x 8192 x 2048 22.9 / 26.7 (128x128), 2048 x 2048 x 1024
-  // 14.2 / 16.9 (128x128), 1024 x 4096 x 4096 38.8 / 45.1 (128x128).  The 64x64 block loses to
-  // entry 6 where entry 6 fits (128 x 8192 x 2048: 13.6 against 12.5 us).
+  // 14.2 / 16.9 (128x128), 1024 x 4096 x 4096 38.8 / 45.1 (128x128).
   if (big_ok && a.K >= 1024)
-    for (int i = 0; i < kNumBig; ++i) {
-      if (kBigBM[i] == 64 && kBigBN[i] == 64 && prefer32) continue;
+    for (int i = 0; i < kBigAutoCount; ++i) {
       const int64_t tiles = batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]);
       const double cost = (double)cdiv(tiles, cus) * kBigBM[i] * kBigBN[i] / kBigRate[i];
       if (cost < best_cost) { best_cost = cost; best = kBigCfg + i; }
