@@ -140,7 +140,10 @@ struct BigTile {
   }
   // Load p of this thread for the stage at K element k into ring slot `slot`.
   __device__ static __forceinline__ void issue_one(char* smem, const Src& src, int slot, int64_t k, int p) {
-    const int wbase = threadIdx.x & ~63;
+    // Wave-uniform by construction; read from lane 0 so that the LDS destination (M0) is scalar
+    // arithmetic instead of a vector value moved to a scalar register for every load (128x64
+    // blocks at M=1024, N=2048, K=8192: 47.7 -> 44.6 us in a same-box A/B, same bits).
+    const int wbase = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63);
     const T* ptr;
     if (p < A_LOADS) {
       const int r = src.r0 + 32 * p;

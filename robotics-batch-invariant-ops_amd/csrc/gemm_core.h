@@ -335,7 +335,7 @@ struct GemmTile {
   __device__ static __forceinline__ void direct_load(char* stage, const AS& as, const BSource<T>& B,
                                                      int64_t k0) {
     const int t = threadIdx.x;
-    const int wbase = t & ~63;
+    const int wbase = __builtin_amdgcn_readfirstlane(t & ~63);  // wave-uniform: scalar LDS offsets
 #pragma unroll
     for (int p = 0; p < A_SLOTS / THREADS; ++p) {
       const T* src = as.at(p) + k0;

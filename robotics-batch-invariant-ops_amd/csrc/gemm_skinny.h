@@ -229,7 +229,7 @@ struct SkinnyTile {
     Acc acc;
     Math::zero(acc);
     if (KT == 0) return acc;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar LDS offsets
     const int lane = threadIdx.x & 63;
     // This thread's load i of a stage: instruction w + WAVES*i = (K step u, part p).  Lane l
     // writes slot l of the part's 64 slots: row 8*part + l/8, holding logical chunk
