@@ -192,17 +192,26 @@ int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t 
                      const void* mask, int mask_dtype, int64_t mB, int64_t mH, int64_t mI, int64_t mJ,
                      int causal, float scale, void* out, void* stream);
 
+/* Tile order of biops_varlen_sdpa_fused: writes plan[5] entries (the plan's count of 128-row
+ * query tiles) into the host array `order`, one per (sequence, query tile), as
+ * (item << 32) | tile, sorted by the number of keys the tile sees under `causal`, most first
+ * (ties in plan order), and returns the count, or <0 on a malformed plan.  The order only
+ * schedules work: every tile's bits are the same in any order.  No reference counterpart (the
+ * reference launches one eager SDPA per sequence). */
+int64_t biops_varlen_fused_order(const int64_t* plan, int causal, int64_t* order);
+
 /* Packed varlen attention with the fused kernel: same arguments as biops_varlen_sdpa without
- * the workspace (the plan from biops_varlen_plan; biops_varlen_fused_supported).  out rows outside every
- * sequence are not written.  Same layout conditions as biops_sdpa_fused.
+ * the workspace (the plan from biops_varlen_plan; biops_varlen_fused_supported), plus `dorder`,
+ * the device copy of biops_varlen_fused_order's array for the same plan and causal mode.  out
+ * rows outside every sequence are not written.  Same layout conditions as biops_sdpa_fused.
  * Replaces varlen_scaled_dot_product_attention_batch_invariant (batch_invariant_ops.py:1216-1344). */
 int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
                             const void* q, int64_t sq_t, int64_t sq_h,
                             const void* k, int64_t sk_t, int64_t sk_h,
                             const void* v, int64_t sv_t, int64_t sv_h,
                             void* out, int64_t so_t, int64_t so_h,
-                            const int64_t* dplan, const int64_t* hplan, int causal, float scale,
-                            void* stream);
+                            const int64_t* dplan, const int64_t* hplan, const int64_t* dorder,
+                            int causal, float scale, void* stream);
 
 /* Workspace bytes biops_sdpa needs (the materialised score/probability matrices). */
 int64_t biops_sdpa_workspace_size(int dtype, int64_t batch, int64_t hq, int64_t lq, int64_t lk);
@@ -229,7 +238,8 @@ int biops_sdpa(int dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, in
  * cumulative offsets (nseq+1 entries each, validated by the caller), writes the per-sequence
  * work list used by biops_varlen_sdpa into `plan` (host int64 array of
  * biops_varlen_plan_len(nseq) entries) and returns the workspace bytes needed, or <0 on a
- * malformed offset list.  Empty query or key ranges are dropped (their rows stay zero). */
+ * malformed offset list.  Empty query or key ranges are dropped (their rows stay zero).
+ * Header words: items, QK tiles, PV tiles, score rows, score elements, 128-row query tiles. */
 int64_t biops_varlen_plan_len(int64_t nseq);
 int64_t biops_varlen_plan(int64_t nseq, const int64_t* cu_q, const int64_t* cu_kv,
                           int64_t hq, int64_t dv, int dtype, int64_t* plan);

@@ -747,15 +747,23 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     # sequences, or of a sequence with an empty key range, must read as zero.
     every_row_written = fused and cu_q[-1] == query.shape[1] and bool(((kv_lens > 0) | (q_lens == 0)).all())
     output = (torch.empty if every_row_written else torch.zeros)(out_shape, dtype=value.dtype, device=value.device)
-    # the work list goes up from pinned memory without blocking the host (torch's pinned-memory
-    # cache keeps the staging block until the copy has run)
-    dplan = torch.from_numpy(plan).pin_memory().to(query.device, non_blocking=True)
     if is_causal:
         causal = nat.CAUSAL_BOTTOM_RIGHT if causal_name == "BottomRight" else nat.CAUSAL_TOP_LEFT
     else:
         causal = nat.CAUSAL_NONE
     scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
     if fused:
+        import numpy as np
+
+        # work list and tile order (longest key range first) in one upload from pinned memory,
+        # without blocking the host (torch's pinned-memory cache keeps the staging block until
+        # the copy has run)
+        host = np.empty(plan.size + int(plan[5]), dtype=np.int64)
+        host[: plan.size] = plan
+        lib = nat.load()
+        if lib.biops_varlen_fused_order(plan.ctypes.data, causal, host[plan.size :].ctypes.data) < 0:
+            raise ValueError(lib.biops_last_error().decode())
+        dev = torch.from_numpy(host).pin_memory().to(query.device, non_blocking=True)
         nat.call(
             "biops_varlen_sdpa_fused",
             nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
@@ -763,10 +771,11 @@ def varlen_scaled_dot_product_attention_batch_invariant(
             k.data_ptr(), k.stride(1), k.stride(2),
             v.data_ptr(), v.stride(1), v.stride(2),
             output.data_ptr(), output.stride(1), output.stride(2),
-            dplan.data_ptr(), plan.ctypes.data, causal, float(scale_value),
+            dev.data_ptr(), plan.ctypes.data, dev[plan.size :].data_ptr(), causal, float(scale_value),
             nat.stream_of(output),
         )
         return output
+    dplan = torch.from_numpy(plan).pin_memory().to(query.device, non_blocking=True)
     workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
     nat.call(
         "biops_varlen_sdpa",

@@ -164,7 +164,7 @@ extern "C" int64_t biops_varlen_plan(int64_t nseq, const int64_t* cu_q, const in
     set_error("invalid varlen plan arguments");
     return -1;
   }
-  int64_t items = 0, qk = 0, pv = 0, rows = 0, selems = 0;
+  int64_t items = 0, qk = 0, pv = 0, rows = 0, selems = 0, qtiles = 0;
   for (int64_t s = 0; s < nseq; ++s) {
     const int64_t q0 = cu_q[s], ql = cu_q[s + 1] - cu_q[s];
     const int64_t k0 = cu_kv[s], kl = cu_kv[s + 1] - cu_kv[s];
@@ -180,10 +180,12 @@ extern "C" int64_t biops_varlen_plan(int64_t nseq, const int64_t* cu_q, const in
     pv += hq * cdiv(ql, kVarlenBM) * cdiv(dv, kVarlenBN);
     rows += hq * ql;
     selems += hq * ql * varlen_score_ld(kl);
+    qtiles += cdiv(ql, kVarlenBM);
     ++items;
   }
   plan[0] = items; plan[1] = qk; plan[2] = pv; plan[3] = rows; plan[4] = selems;
-  plan[5] = plan[6] = plan[7] = 0;
+  plan[5] = qtiles;
+  plan[6] = plan[7] = 0;
   return selems * elt;
 }
 

@@ -24,6 +24,9 @@
 // inside the chunk permuted the same way for P and for V), so P goes from the accumulators to
 // the next MFMA without passing through LDS.  V fragments come from LDS with the transposing
 // 64-bit read.
+#include <algorithm>
+#include <vector>
+
 #include "gemm.h"
 #include "rowops.h"
 
@@ -32,7 +35,8 @@ namespace biops {
 struct FusedArgs {
   const void* q; const void* k; const void* v; void* out;
   const void* mask;
-  const int64_t* plan;  // varlen work list (VARLEN kernels)
+  const int64_t* plan;   // varlen work list (VARLEN kernels)
+  const int64_t* order;  // varlen tile order: (item << 32) | query tile, longest key range first
   int64_t hq, group, hkv, lq, lk, d, dv;
   // element strides: batch (unused for varlen), head, row (token)
   int64_t sqB, sqH, sqL, skB, skH, skL, svB, svH, svL, soB, soH, soL;
@@ -84,39 +88,51 @@ struct FusedGeom {
   int64_t ql, kl; // sequence lengths
 };
 
+// Tile order (workgroup w takes tile w; the dispatcher deals workgroups to the 8 XCDs in turn,
+// so XCD x runs tiles x, x + 8, ...).  Causal tiles differ in cost by up to the number of query
+// tiles, so the order is longest key range first, which keeps long tiles out of the launch's
+// tail:
+//   dense: (batch, head) pairs in chunks of kFusedChunk; inside a chunk, query tiles from the
+//          last (longest causal key range) to the first, all pairs of the chunk per level.  When
+//          the chunk holds a multiple of 8 pairs, XCD x takes pairs x*n/8 .. (x+1)*n/8 - 1 of it
+//          at every level, so a head's key/value rows stay in one XCD's L2;
+//   varlen: the host sorts (sequence, query tile) entries by key range
+//          (biops_varlen_fused_order); the heads of an entry are consecutive tiles.
+constexpr int64_t kFusedChunk = 64;
+
 template <typename T, bool VARLEN>
 __device__ __forceinline__ bool fused_geom(const FusedArgs& a, int64_t t, FusedGeom& g) {
   constexpr int E = sizeof(T);
   int64_t h, qt, qstart = 0, kstart = 0, b = 0;
   if constexpr (VARLEN) {
-    // item whose first tile (plan word 6) is the last one <= t
-    int64_t lo = 0, hi = a.items - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) >> 1;
-      if (a.plan[kPlanHeader + kPlanStride * mid + 6] <= t) lo = mid;
-      else hi = mid - 1;
-    }
-    const int64_t* p = a.plan + kPlanHeader + kPlanStride * lo;
+    const int64_t e = a.order[t / a.hq];
+    const int64_t item = e >> 32;
+    qt = e & 0xffffffffLL;
+    if (item < 0 || item >= a.items) return false;
+    const int64_t* p = a.plan + kPlanHeader + kPlanStride * item;
     g.ql = p[1];
     g.kl = p[3];
     qstart = p[0];
     kstart = p[2];
-    const int64_t local = t - p[6];
-    const int64_t qtiles = cdiv(g.ql, kFusedBM);
-    if (local < 0 || local >= qtiles * a.hq) return false;
-    qt = qtiles - 1 - local / a.hq;  // longest key ranges first (causal)
-    h = local % a.hq;
+    if (qt >= cdiv(g.ql, kFusedBM)) return false;
+    h = t % a.hq;
   } else {
     g.ql = a.lq;
     g.kl = a.lk;
     const int64_t qtiles = cdiv(a.lq, kFusedBM);
-    // heads sharing a key/value head are adjacent; longest key ranges first within a head
-    const int64_t gi = t % a.group;
-    int64_t rest = t / a.group;
-    qt = qtiles - 1 - rest % qtiles;
-    rest /= qtiles;
-    const int64_t hk = rest % a.hkv;
-    b = rest / a.hkv;
+    const int64_t pairs = a.tiles / qtiles;
+    const int64_t chunk = t / (kFusedChunk * qtiles);
+    const int64_t first = chunk * kFusedChunk;
+    const int64_t n = pairs - first < kFusedChunk ? pairs - first : kFusedChunk;
+    const int64_t r = t - chunk * kFusedChunk * qtiles;
+    const int64_t j = r % n;
+    qt = qtiles - 1 - r / n;
+    // pair index: (batch, kv head, head in group), heads sharing a key/value head adjacent
+    int64_t pair = first + ((n & 7) == 0 ? (j & 7) * (n >> 3) + (j >> 3) : j);
+    const int64_t gi = pair % a.group;
+    pair /= a.group;
+    const int64_t hk = pair % a.hkv;
+    b = pair / a.hkv;
     h = hk * a.group + gi;
   }
   const int64_t hk = h / a.group;
@@ -171,7 +187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves
 void fused_attn_kernel(FusedArgs a) {
   using F = FusedTile<T, DP, DVP>;
   __shared__ __attribute__((aligned(16))) char smem[F::LDS_BYTES];
-  const int64_t t = xcd_slot(blockIdx.x, gridDim.x);
+  const int64_t t = blockIdx.x;
   if (t >= a.tiles) return;
   FusedGeom g;
   if (!fused_geom<T, VARLEN>(a, t, g)) return;
@@ -521,9 +537,8 @@ void fused_attn_kernel(FusedArgs a) {
 
 template <typename T, int DP, int DVP, int MASK, bool VARLEN>
 static int launch_fused_t(const FusedArgs& a, hipStream_t s) {
-  const int64_t grid = cdiv(a.tiles, 8) * 8;
-  if (grid > 0x7fffffffLL) return fail(BIOPS_ERR_SIZE, "too many attention tiles");
-  hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  if (a.tiles > 0x7fffffffLL) return fail(BIOPS_ERR_SIZE, "too many attention tiles");
+  hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN>), dim3((unsigned)a.tiles), dim3(256), 0, s, a);
   return check_launch("fused_attn_kernel");
 }
 
@@ -597,7 +612,7 @@ extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hk
   if (!block_fits(skL) || !block_fits(svL) || !block_fits(sqL) || lq >= (int64_t(1) << 31) || lk >= (int64_t(1) << 31))
     return fail(BIOPS_ERR_LAYOUT, "fused attention row strides or lengths too large");
   FusedArgs a{};
-  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = mask; a.plan = nullptr;
+  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = mask; a.plan = nullptr; a.order = nullptr;
   a.hq = hq; a.group = hq / hkv; a.hkv = hkv; a.lq = lq; a.lk = lk; a.d = d; a.dv = dv;
   a.sqB = sqB; a.sqH = sqH; a.sqL = sqL; a.skB = skB; a.skH = skH; a.skL = skL;
   a.svB = svB; a.svH = svH; a.svL = svL;
@@ -612,18 +627,52 @@ extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hk
   return launch_fused<2, false>(dtype, a, s);
 }
 
+extern "C" int64_t biops_varlen_fused_order(const int64_t* plan, int causal, int64_t* order) {
+  if (!plan || !order || plan[0] < 0 || plan[5] < 0) {
+    set_error("invalid varlen plan or order buffer");
+    return -1;
+  }
+  struct Entry { int64_t keys, code; };
+  std::vector<Entry> list;
+  list.reserve((size_t)plan[5]);
+  for (int64_t i = 0; i < plan[0]; ++i) {
+    const int64_t* p = plan + kPlanHeader + kPlanStride * i;
+    const int64_t ql = p[1], kl = p[3];
+    const int64_t shift = causal == BIOPS_CAUSAL_BOTTOM_RIGHT ? kl - ql : 0;
+    const int64_t qtiles = cdiv(ql, kFusedBM);
+    for (int64_t qt = 0; qt < qtiles; ++qt) {
+      int64_t keys = kl;
+      if (causal != BIOPS_CAUSAL_NONE) {  // keys of the tile's last row (row_lim in the kernel)
+        const int64_t last = (ql < (qt + 1) * kFusedBM ? ql : (qt + 1) * kFusedBM) - 1;
+        keys = last + shift + 1;
+        keys = keys < 0 ? 0 : (keys > kl ? kl : keys);
+      }
+      list.push_back({keys, (i << 32) | qt});
+    }
+  }
+  if ((int64_t)list.size() != plan[5]) {
+    set_error("varlen plan's query-tile count (word 5) does not match its items");
+    return -1;
+  }
+  std::stable_sort(list.begin(), list.end(), [](const Entry& x, const Entry& y) { return x.keys > y.keys; });
+  for (size_t k = 0; k < list.size(); ++k) order[k] = list[k].code;
+  return (int64_t)list.size();
+}
+
 extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
                                        const void* q, int64_t sq_t, int64_t sq_h, const void* k,
                                        int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t,
                                        int64_t sv_h, void* out, int64_t so_t, int64_t so_h,
-                                       const int64_t* dplan, const int64_t* hplan, int causal,
-                                       float scale, void* stream) {
+                                       const int64_t* dplan, const int64_t* hplan,
+                                       const int64_t* dorder, int causal, float scale, void* stream) {
   if (!biops_varlen_fused_supported(dtype, d, dv))
     return fail(BIOPS_ERR_DTYPE, "fused varlen attention takes bf16/fp16 with head dims <= 128, multiples of 8");
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(BIOPS_ERR_ARG, "invalid varlen head configuration");
-  if (!dplan || !hplan) return fail(BIOPS_ERR_ARG, "null plan");
+  if (!dplan || !hplan || !dorder) return fail(BIOPS_ERR_ARG, "null plan or tile order");
   const int64_t items = hplan[0];
   if (items == 0) return BIOPS_OK;
+  if (hplan[5] <= 0 || hplan[5] * hq != hplan[2])
+    return fail(BIOPS_ERR_ARG, "plan without its query-tile count (word 5)");
   for (int64_t i = 0; i < items; ++i) {  // sequence lengths are 32-bit inside the kernel
     const int64_t* p = hplan + kPlanHeader + kPlanStride * i;
     if (p[1] >= (int64_t(1) << 31) || p[3] >= (int64_t(1) << 31))
@@ -635,14 +684,12 @@ extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64
   if (!block_fits(sk_t) || !block_fits(sv_t) || !block_fits(sq_t))
     return fail(BIOPS_ERR_LAYOUT, "fused attention row strides too large");
   FusedArgs a{};
-  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = nullptr; a.plan = dplan;
+  a.q = q; a.k = k; a.v = v; a.out = out; a.mask = nullptr; a.plan = dplan; a.order = dorder;
   a.hq = hq; a.group = hq / hkv; a.hkv = hkv; a.d = d; a.dv = dv;
   a.sqL = sq_t; a.sqH = sq_h; a.skL = sk_t; a.skH = sk_h; a.svL = sv_t; a.svH = sv_h;
   a.soL = so_t; a.soH = so_h;
   a.items = items;
-  // With dv <= 128 the plan's PV tile count (one 128-row tile per head and query block) is the
-  // fused kernel's tile count, and word 6 of each item its first tile.
-  a.tiles = hplan[2];
+  a.tiles = hplan[5] * hq;  // one tile per head and 128-row query tile
   a.scale = scale;
   a.causal = causal;
   return launch_fused<0, true>(dtype, a, (hipStream_t)stream);

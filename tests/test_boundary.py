@@ -175,6 +175,36 @@ def test_varlen_plan_work_list():
     assert rows == 4 * 5 + 4 * 130
     assert selems == 4 * 5 * 8 + 4 * 130 * 136
     assert ws == selems * 2
+    assert p[5] == 1 + 2  # 128-row query tiles: 5 rows, then 130 rows
+
+
+def fused_order(p, causal):
+    L = lib()
+    order = np.full(int(p[5]), -1, dtype=np.int64)
+    n = L.biops_varlen_fused_order(p.ctypes.data, causal, order.ctypes.data)
+    return n, [(int(e) >> 32, int(e) & 0xFFFFFFFF) for e in order]
+
+
+def test_varlen_fused_order_longest_key_range_first():
+    # items: (q 5, kv 7) and (q 130, kv 129); entries are (item, query tile)
+    _, p = plan([0, 5, 5, 305, 435], [0, 7, 11, 11, 140], hq=4, dv=24)
+    # bottom-right: item 1's tiles see keys up to row + (129 - 130) + 1: 127 and 129 keys,
+    # item 0's one tile 4 + 2 + 1 = 7 keys
+    assert fused_order(p, nat.CAUSAL_BOTTOM_RIGHT) == (3, [(1, 1), (1, 0), (0, 0)])
+    # top-left: 128 and min(130, 129) keys against 5
+    assert fused_order(p, nat.CAUSAL_TOP_LEFT) == (3, [(1, 1), (1, 0), (0, 0)])
+    # no mask: every tile of a sequence sees all its keys; ties keep plan order
+    assert fused_order(p, nat.CAUSAL_NONE) == (3, [(1, 0), (1, 1), (0, 0)])
+    # a short sequence after a long one still goes after its longer tiles
+    _, p = plan([0, 300, 340], [0, 300, 340], hq=2, dv=8)
+    assert fused_order(p, nat.CAUSAL_BOTTOM_RIGHT) == (4, [(0, 2), (0, 1), (0, 0), (1, 0)])
+
+
+def test_varlen_fused_order_rejects_an_inconsistent_plan():
+    _, p = plan([0, 5, 135], [0, 7, 140])
+    p[5] += 1
+    n, _ = fused_order(p, nat.CAUSAL_NONE)
+    assert n < 0 and b"word 5" in lib().biops_last_error()
 
 
 def test_varlen_plan_rejects_decreasing_offsets():
