@@ -147,17 +147,12 @@ __device__ __forceinline__ bool fused_geom(const FusedArgs& a, int64_t t, FusedG
   return true;
 }
 
-// Round two fp32 values to T (and back to fp32) -- one paired conversion for bf16.
+// Round two fp32 values to T (and back to fp32): one conversion each (for bf16, the pair
+// conversion with +0 in the low half).
 template <typename T>
 __device__ __forceinline__ void round2(float& x0, float& x1) {
-  if constexpr (std::is_same<T, bf16_t>::value) {
-    const uint32_t pk = f32x2_to_bf16x2_bits(x0, x1);
-    x0 = __uint_as_float(pk << 16);
-    x1 = __uint_as_float(pk & 0xffff0000u);
-  } else {
-    x0 = Num<T>::round(x0);
-    x1 = Num<T>::round(x1);
-  }
+  x0 = Num<T>::round(x0);
+  x1 = Num<T>::round(x1);
 }
 
 // First MFMA of a chain: the accumulator input is the constant zero.

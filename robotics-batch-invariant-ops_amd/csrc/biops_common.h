@@ -58,7 +58,8 @@ template <> struct Num<bf16_t> {
   static constexpr int kBytes = 2;
   __device__ static __forceinline__ float load(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
   __device__ static __forceinline__ void store(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
-  __device__ static __forceinline__ float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+  // One conversion: with +0 in the low half, the pair's bits are the rounded value as fp32.
+  __device__ static __forceinline__ float round(float v) { return __uint_as_float(f32x2_to_bf16x2_bits(0.f, v)); }
   __device__ static __forceinline__ float from_bits(uint32_t b) { return bf16_bits_to_f32((uint16_t)b); }
   __device__ static __forceinline__ uint16_t to_bits(float v) { return f32_to_bf16_bits(v); }
 };
