@@ -25,6 +25,8 @@
 // the next MFMA without passing through LDS.  V fragments come from LDS with the transposing
 // 64-bit read.
 #include <algorithm>
+#include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "gemm.h"
@@ -44,6 +46,7 @@ struct FusedArgs {
   int64_t items, tiles;
   float scale;
   int causal;
+  int pow2;  // the scale is 2^k, -8 <= k <= 0 (bf16 kernels without an additive mask)
 };
 
 constexpr int kFusedBM = 128;  // query rows per workgroup
@@ -177,9 +180,16 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
 template <int DP, int DVP>
 constexpr int fused_waves_per_eu() { return DP > 128 || DVP > 128 ? 1 : 2; }
 
-template <typename T, int DP, int DVP, int MASK, bool VARLEN>
+// P2: the scale is a power of two 2^k (-8 <= k <= 0), bf16 inputs, no additive mask.  Then
+// round(round(S) * scale) = round(S) * scale exactly whenever the product is a normal number (a
+// bf16 significand survives the power of two, and bf16 has fp32's exponent range), so the kernel
+// keeps the scores in units of round(S) and folds the scale into the base change of the
+// exponentials: scale * log2(e) is exact too, and so are the products with it.  Only a product
+// below 2^-126 in magnitude (a bf16 denormal) skips its rounding.
+template <typename T, int DP, int DVP, int MASK, bool VARLEN, bool P2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves_per_eu<DP, DVP>(), 2)))
 void fused_attn_kernel(FusedArgs a) {
+  static_assert(!P2 || (MASK != 2 && std::is_same<T, bf16_t>::value), "power-of-two scale path");
   using F = FusedTile<T, DP, DVP>;
   __shared__ __attribute__((aligned(16))) char smem[F::LDS_BYTES];
   const int64_t t = blockIdx.x;
@@ -353,9 +363,11 @@ void fused_attn_kernel(FusedArgs a) {
     for (int r = 0; r < 16; r += 2) {
       float s0 = acc[r], s1 = acc[r + 1];
       round2<T>(s0, s1);
-      s0 *= a.scale;
-      s1 *= a.scale;
-      round2<T>(s0, s1);
+      if constexpr (!P2) {
+        s0 *= a.scale;
+        s1 *= a.scale;
+        round2<T>(s0, s1);
+      }
       if constexpr (!decltype(open)::value) {
         const int o = 8 * (r >> 2) + (r & 3);
         s0 = o < rel ? s0 : -INFINITY;
@@ -383,6 +395,8 @@ void fused_attn_kernel(FusedArgs a) {
   // Running maximum m (shared by both half-wavefronts of a row) and this half's sum l of
   // exp(s - m), rescaled when m grows; 32-key steps in order.
   float m = -INFINITY, l = 0.f;
+  // base change of the exponentials (scores in units of round(S) under P2)
+  const float kexp = P2 ? a.scale * kLog2e : kLog2e;
   auto stats = [&](const f32x16_t& sc) {
     float bm = sc[0];
 #pragma unroll
@@ -390,11 +404,11 @@ void fused_attn_kernel(FusedArgs a) {
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     // m = -inf until a visible key appears: the shift stays 0 and every term is exp(-inf) = 0
     const float mn = fmaxf(m, bm);
-    const float sh = (mn == -INFINITY ? 0.f : mn) * kLog2e;
-    const float corr = __builtin_amdgcn_exp2f(m * kLog2e - sh);
+    const float sh = (mn == -INFINITY ? 0.f : mn) * kexp;
+    const float corr = __builtin_amdgcn_exp2f(m * kexp - sh);
     float part = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kLog2e, -sh));
+    for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kexp, -sh));
     l = l * corr + part;
     m = mn;
   };
@@ -438,7 +452,7 @@ void fused_attn_kernel(FusedArgs a) {
   const float lt = l + __shfl_xor(l, 32, 64);
   const bool dead = (m == -INFINITY) || (lt == 0.f);
   const float inv = dead ? 0.f : 1.0f / lt;
-  const float shl2e = (m == -INFINITY ? 0.f : m) * kLog2e;
+  const float shl2e = (m == -INFINITY ? 0.f : m) * kexp;
 
   // ---------------------------------------------------------------- pass 2: P V ----
   f32x16_t oacc[F::OF];
@@ -465,7 +479,7 @@ void fused_attn_kernel(FusedArgs a) {
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * c2 + e], kLog2e, -shl2e)) * inv;
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * c2 + e], kexp, -shl2e)) * inv;
       const u32x4_t pa = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
                           pack2<T>(p[6], p[7])};
       const int row = 16 * (2 * hb + c2) + vrow;
@@ -533,7 +547,11 @@ void fused_attn_kernel(FusedArgs a) {
 template <typename T, int DP, int DVP, int MASK, bool VARLEN>
 static int launch_fused_t(const FusedArgs& a, hipStream_t s) {
   if (a.tiles > 0x7fffffffLL) return fail(BIOPS_ERR_SIZE, "too many attention tiles");
-  hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN>), dim3((unsigned)a.tiles), dim3(256), 0, s, a);
+  constexpr bool kP2 = MASK != 2 && std::is_same<T, bf16_t>::value;
+  if (kP2 && a.pow2)
+    hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN, kP2>), dim3((unsigned)a.tiles), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((fused_attn_kernel<T, DP, DVP, MASK, VARLEN, false>), dim3((unsigned)a.tiles), dim3(256), 0, s, a);
   return check_launch("fused_attn_kernel");
 }
 
@@ -561,6 +579,14 @@ static int launch_fused(int dtype, const FusedArgs& a, hipStream_t s) {
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// scale = 2^k with -8 <= k <= 0 (the fused kernels' exact power-of-two path); the environment
+// variable BIOPS_ATTN_GENERIC_SCALE=1 turns the path off (tests compare the two).
+static int pow2_scale(float scale) {
+  int e = 0;
+  if (!(scale > 0.f) || std::frexp(scale, &e) != 0.5f || e - 1 < -8 || e - 1 > 0) return 0;
+  const char* env = std::getenv("BIOPS_ATTN_GENERIC_SCALE");
+  return (env && env[0] == '1') ? 0 : 1;
+}
 static bool mult8(int64_t x) { return (x & 7) == 0; }
 // Byte offsets inside one key block (64 rows) are 32-bit.
 static bool block_fits(int64_t row_stride) { return row_stride >= 0 && 2 * kFusedBN * row_stride < (int64_t(1) << 31); }
@@ -616,6 +642,7 @@ extern "C" int biops_sdpa_fused(int dtype, int64_t batch, int64_t hq, int64_t hk
   a.tiles = batch * hq * cdiv(lq, kFusedBM);
   a.scale = scale;
   a.causal = causal;
+  a.pow2 = pow2_scale(scale);
   hipStream_t s = (hipStream_t)stream;
   if (!mask) return launch_fused<0, false>(dtype, a, s);
   if (mask_dtype == BIOPS_BOOL) return launch_fused<1, false>(dtype, a, s);
@@ -687,5 +714,6 @@ extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64
   a.tiles = hplan[5] * hq;  // one tile per head and 128-row query tile
   a.scale = scale;
   a.causal = causal;
+  a.pow2 = pow2_scale(scale);
   return launch_fused<0, true>(dtype, a, (hipStream_t)stream);
 }

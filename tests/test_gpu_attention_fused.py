@@ -232,3 +232,57 @@ def test_fused_sdpa_uniform_attention_averages_values():
     prefix = vd.cumsum(2) / torch.arange(1, 101, dtype=torch.float64).view(1, 1, 100, 1)
     # P = round(1/n) for every visible key: the output is sum(round(1/n) * v), within 4 ulps
     assert_close_scaled(out, prefix, rel=4 * ULP[dtype], abs_scale=4 * ULP[dtype] * float(vd.abs().max()))
+
+
+POW2_CASES = {
+    # name: (B, Hq, Hkv, L, D, explicit scale, mask kind)
+    "d64_causal": (2, 4, 2, 300, 64, None, "causal"),
+    "d64_boolean_mask": (2, 4, 4, 190, 64, None, "boolean"),
+    "d256": (1, 2, 1, 200, 256, None, "causal"),
+    "d16": (1, 2, 2, 129, 16, None, None),
+    "scale_half": (1, 2, 2, 150, 128, 0.5, "causal"),
+    "scale_one": (1, 2, 2, 150, 128, 1.0, None),
+    "scale_2^-8": (1, 2, 2, 150, 128, 2.0 ** -8, "causal"),
+}
+
+
+@pytest.mark.parametrize("case", sorted(POW2_CASES))
+def test_power_of_two_scale_path_equals_generic_path(case, monkeypatch):
+    """bf16 attention with a scale 2^k (-8 <= k <= 0) and no additive mask takes the fused
+    kernels' power-of-two path (scores kept in units of round(S), the scale folded into the
+    exponentials' base change); for scores of normal magnitude its bits equal the generic path's
+    (round(round(S) * scale) per score), selected with BIOPS_ATTN_GENERIC_SCALE=1."""
+    B, Hq, Hkv, L, D, scale, kind = POW2_CASES[case]
+    dtype = torch.bfloat16
+    seed = 8500 + sorted(POW2_CASES).index(case) * 10
+    q = randn(B, Hq, L, D, seed=seed, dtype=dtype, scale=2.0).cuda()
+    k = randn(B, Hkv, L, D, seed=seed + 1, dtype=dtype).cuda()
+    v = randn(B, Hkv, L, D, seed=seed + 2, dtype=dtype).cuda()
+    kw = dict(scale=scale, enable_gqa=Hq != Hkv)
+    if kind == "causal":
+        kw["is_causal"] = True
+    elif kind == "boolean":
+        g = torch.Generator().manual_seed(seed + 3)
+        kw["attn_mask"] = (torch.rand(B, 1, L, L, generator=g) > 0.25).cuda()
+    fast = sdpa(q, k, v, **kw)
+    monkeypatch.setenv("BIOPS_ATTN_GENERIC_SCALE", "1")
+    generic = sdpa(q, k, v, **kw)
+    assert_bitwise(fast, generic, f"{case}: power-of-two path vs generic path")
+    ref = oracle.sdpa(q.cpu(), k.cpu(), v.cpu(), **{n: (x.cpu() if torch.is_tensor(x) else x) for n, x in kw.items()})
+    check_attention(fast, ref, v.cpu(), dtype, what=f"{case} vs oracle")
+
+
+def test_power_of_two_scale_path_varlen(monkeypatch):
+    lengths = (300, 64, 1, 129, 513, 77)
+    dtype = torch.bfloat16
+    q = randn(1, sum(lengths), 8, 64, seed=8600, dtype=dtype, scale=2.0).cuda()
+    k = randn(1, sum(lengths), 2, 64, seed=8601, dtype=dtype).cuda()
+    v = randn(1, sum(lengths), 2, 64, seed=8602, dtype=dtype).cuda()
+    cu = _offsets(lengths).cuda()
+    for causal_type in (None, "BottomRight"):
+        kw = dict(is_causal=causal_type is not None, causal_type=causal_type)
+        monkeypatch.delenv("BIOPS_ATTN_GENERIC_SCALE", raising=False)
+        fast = varlen(q, k, v, cu, cu, **kw)
+        monkeypatch.setenv("BIOPS_ATTN_GENERIC_SCALE", "1")
+        generic = varlen(q, k, v, cu, cu, **kw)
+        assert_bitwise(fast, generic, f"varlen {causal_type}: power-of-two path vs generic path")
