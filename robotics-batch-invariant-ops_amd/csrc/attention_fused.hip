@@ -320,16 +320,48 @@ void fused_attn_kernel(FusedArgs a) {
   // Scores of keys 32 hb .. 32 hb + 31 of a block: acc[r] is key 64 blk + 32 hb + 8(r/4) +
   // 4 hf + r%4 of this lane's row.  s_mfma produces the raw fp32 S (one MFMA chain over the
   // head dimension); transform applies the reference's roundings and masks in place.
-  auto s_mfma = [&](int buf, int hb, f32x16_t& acc) {
+  // The K fragments of a chain are read from LDS before its first MFMA (a scheduling barrier
+  // keeps the compiler from sinking each read next to its MFMA, which would expose one LDS
+  // latency per MFMA).
+  auto s_frags = [&](int buf, int hb, u32x4_t (&kf)[F::QF]) {
     const char* kb = kbuf0 + buf * F::K_BYTES;
-    {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, hf));
-      acc = mfma_first<T>(kf, qf[0]);
-    }
 #pragma unroll
-    for (int cc = 1; cc < F::QF; ++cc) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf));
-      Mfma<T>::step(acc, kf, qf[cc]);
+    for (int cc = 0; cc < F::QF; ++cc)
+      kf[cc] = *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf));
+  };
+  auto s_chain = [&](const u32x4_t (&kf)[F::QF], f32x16_t& acc) {
+    acc = mfma_first<T>(kf[0], qf[0]);
+#pragma unroll
+    for (int cc = 1; cc < F::QF; ++cc) Mfma<T>::step(acc, kf[cc], qf[cc]);
+  };
+  // (Masked kernels leave the reads to the compiler: their mask words leave no registers for
+  // the fragments.)
+  auto s_mfma = [&](int buf, int hb, f32x16_t& acc) {
+    if constexpr (MASK == 0) {
+      u32x4_t kf[F::QF];
+      s_frags(buf, hb, kf);
+      __builtin_amdgcn_sched_barrier(0);
+      s_chain(kf, acc);
+    } else {
+      const char* kb = kbuf0 + buf * F::K_BYTES;
+      acc = mfma_first<T>(*reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, hf)), qf[0]);
+#pragma unroll
+      for (int cc = 1; cc < F::QF; ++cc)
+        Mfma<T>::step(acc, *reinterpret_cast<const u32x4_t*>(kb + F::k_off(32 * hb + l32, 2 * cc + hf)), qf[cc]);
+    }
+  };
+  // both halves of a block: all reads first
+  auto s_mfma2 = [&](int buf, f32x16_t& acc0, f32x16_t& acc1) {
+    if constexpr (MASK != 0) {
+      s_mfma(buf, 0, acc0);
+      s_mfma(buf, 1, acc1);
+    } else {
+      u32x4_t kf0[F::QF], kf1[F::QF];
+      s_frags(buf, 0, kf0);
+      s_frags(buf, 1, kf1);
+      __builtin_amdgcn_sched_barrier(0);
+      s_chain(kf0, acc0);
+      s_chain(kf1, acc1);
     }
   };
   // Raw mask words of the 16 keys of a half-block: MASK 1 -> mw[j] holds the four bytes of keys
@@ -405,11 +437,11 @@ void fused_attn_kernel(FusedArgs a) {
     // m = -inf until a visible key appears: the shift stays 0 and every term is exp(-inf) = 0
     const float mn = fmaxf(m, bm);
     const float sh = (mn == -INFINITY ? 0.f : mn) * kexp;
-    const float corr = __builtin_amdgcn_exp2f(m * kexp - sh);
+    const float corr = __builtin_amdgcn_exp2f(__builtin_fmaf(m, kexp, -sh));
     float part = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) part += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], kexp, -sh));
-    l = l * corr + part;
+    l = __builtin_fmaf(l, corr, part);
     m = mn;
   };
   if (nblk > 0) {
@@ -426,8 +458,7 @@ void fused_attn_kernel(FusedArgs a) {
       mask_words(blk, 0, mw0);
       mask_words(blk, 1, mw1);
       f32x16_t s0, s1;
-      s_mfma(buf, 0, s0);
-      s_mfma(buf, 1, s1);
+      s_mfma2(buf, s0, s1);
       transform(std::true_type{}, blk, 0, s0, mw0);
       stats(s0);
       transform(std::true_type{}, blk, 1, s1, mw1);
