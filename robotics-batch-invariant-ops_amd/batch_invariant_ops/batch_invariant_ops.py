@@ -656,18 +656,27 @@ def _offsets_on_host(cu_q, cu_kv):
     return host_q, np.ascontiguousarray(cu_kv.detach().cpu().numpy(), dtype=np.int64)
 
 
-def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype):
-    import numpy as np
-
+def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal=None):
+    """The work list of biops_varlen_plan in pinned host memory (int64 tensor, ready for an
+    asynchronous upload), followed, when ``order_causal`` is a causal code, by the fused
+    kernel's tile order (biops_varlen_fused_order).  Returns (buffer, plan words, workspace
+    bytes); the buffer's numpy view starts with the plan."""
     nseq = len(cu_q) - 1
     lib = nat.load()
-    plan = np.zeros(lib.biops_varlen_plan_len(nseq), dtype=np.int64)
+    words = int(lib.biops_varlen_plan_len(nseq))
+    # at most total_q / 128 + nseq query tiles (each sequence adds at most one partial tile)
+    extra = int(cu_q[-1]) // 128 + nseq if order_causal is not None else 0
+    buf = torch.empty(words + extra, dtype=torch.int64, pin_memory=torch.cuda.is_available())
+    plan = buf.numpy()
     ws_bytes = lib.biops_varlen_plan(
         nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype), plan.ctypes.data
     )
     if ws_bytes < 0:
         raise ValueError(lib.biops_last_error().decode())
-    return plan, ws_bytes
+    if order_causal is not None and plan[0] > 0:
+        if lib.biops_varlen_fused_order(plan.ctypes.data, order_causal, plan[words:].ctypes.data) < 0:
+            raise ValueError(lib.biops_last_error().decode())
+    return buf, words, ws_bytes
 
 
 def varlen_scaled_dot_product_attention_batch_invariant(
@@ -722,10 +731,8 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     causal_name = getattr(causal_type, "name", None)
     if causal_name is None and causal_type is not None:
         causal_name = str(causal_type).rsplit(".", 1)[-1]
-    q_lens, kv_lens = cu_q[1:] - cu_q[:-1], cu_kv[1:] - cu_kv[:-1]
-    if (q_lens < 0).any() or (kv_lens < 0).any():
-        raise ValueError("cumulative sequence lengths must be nondecreasing")
     if is_causal and causal_name not in {"BottomRight", "TopLeft", None}:
+        q_lens, kv_lens = cu_q[1:] - cu_q[:-1], cu_kv[1:] - cu_kv[:-1]
         if ((q_lens > 0) & (kv_lens > 0) & (q_lens != kv_lens)).any():
             raise ValueError(f"causal type {causal_name!r} requires equal query and KV lengths")
 
@@ -733,9 +740,9 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     head_dim, value_dim = query.shape[3], value.shape[3]
     out_shape = (1, query.shape[1], heads, value_dim)
     if cu_q.size <= 1 or math.prod(out_shape) == 0:
-        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
-    plan, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype)
-    if plan[0] == 0:
+        # still reject decreasing offsets, as the planner does
+        if cu_q.size > 1 and ((cu_q[1:] < cu_q[:-1]).any() or (cu_kv[1:] < cu_kv[:-1]).any()):
+            raise ValueError("cumulative sequence lengths must be nondecreasing")
         return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
 
     def tokens_heads(x):
@@ -743,27 +750,26 @@ def varlen_scaled_dot_product_attention_batch_invariant(
 
     q, k, v = tokens_heads(query), tokens_heads(key), tokens_heads(value)
     fused = _fused_attention_ok(query.dtype, head_dim, value_dim, q, k, v, varlen=True)
-    # The fused kernel writes every row of every sequence it computes; rows outside the
-    # sequences, or of a sequence with an empty key range, must read as zero.
-    every_row_written = fused and cu_q[-1] == query.shape[1] and bool(((kv_lens > 0) | (q_lens == 0)).all())
-    output = (torch.empty if every_row_written else torch.zeros)(out_shape, dtype=value.dtype, device=value.device)
     if is_causal:
         causal = nat.CAUSAL_BOTTOM_RIGHT if causal_name == "BottomRight" else nat.CAUSAL_TOP_LEFT
     else:
         causal = nat.CAUSAL_NONE
+    # planner: validates the offsets (nondecreasing), drops empty sequences, and for the fused
+    # kernel appends the tile order (longest key range first)
+    buf, words, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype, causal if fused else None)
+    plan = buf.numpy()
+    if plan[0] == 0:
+        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
+    # The fused kernel writes every row of every sequence it computes (plan word 3 counts them
+    # per head); rows outside the sequences, or of a sequence with no keys, must read as zero.
+    every_row_written = fused and int(plan[3]) == heads * query.shape[1]
+    output = (torch.empty if every_row_written else torch.zeros)(out_shape, dtype=value.dtype, device=value.device)
     scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
+    # one upload from pinned memory, without blocking the host (torch's pinned-memory cache keeps
+    # the block until the copy has run)
+    used = words + (int(plan[5]) if fused else 0)
+    dev = buf[:used].to(query.device, non_blocking=True)
     if fused:
-        import numpy as np
-
-        # work list and tile order (longest key range first) in one upload from pinned memory,
-        # without blocking the host (torch's pinned-memory cache keeps the staging block until
-        # the copy has run)
-        host = np.empty(plan.size + int(plan[5]), dtype=np.int64)
-        host[: plan.size] = plan
-        lib = nat.load()
-        if lib.biops_varlen_fused_order(plan.ctypes.data, causal, host[plan.size :].ctypes.data) < 0:
-            raise ValueError(lib.biops_last_error().decode())
-        dev = torch.from_numpy(host).pin_memory().to(query.device, non_blocking=True)
         nat.call(
             "biops_varlen_sdpa_fused",
             nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
@@ -771,11 +777,10 @@ def varlen_scaled_dot_product_attention_batch_invariant(
             k.data_ptr(), k.stride(1), k.stride(2),
             v.data_ptr(), v.stride(1), v.stride(2),
             output.data_ptr(), output.stride(1), output.stride(2),
-            dev.data_ptr(), plan.ctypes.data, dev[plan.size :].data_ptr(), causal, float(scale_value),
+            dev.data_ptr(), plan.ctypes.data, dev[words:].data_ptr(), causal, float(scale_value),
             nat.stream_of(output),
         )
         return output
-    dplan = torch.from_numpy(plan).pin_memory().to(query.device, non_blocking=True)
     workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
     nat.call(
         "biops_varlen_sdpa",
@@ -784,7 +789,7 @@ def varlen_scaled_dot_product_attention_batch_invariant(
         k.data_ptr(), k.stride(1), k.stride(2),
         v.data_ptr(), v.stride(1), v.stride(2),
         output.data_ptr(), output.stride(1), output.stride(2),
-        dplan.data_ptr(), plan.ctypes.data, causal, float(scale_value),
+        dev.data_ptr(), plan.ctypes.data, causal, float(scale_value),
         workspace.data_ptr(), workspace.numel(),
         nat.stream_of(output),
     )
