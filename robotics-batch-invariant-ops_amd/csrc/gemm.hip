@@ -62,6 +62,12 @@ static const int kBigBN[kNumBig] = {256, 128, 256, 128, 64, 128, 64};
 // every shape measured (M=64..512 at N=8192, K=2048 and N=2048, K=8192).
 static const double kBigRate[kNumBig] = {1150, 1050, 1050, 850, 700, 720, 480};
 constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weighs
+// With a 16-bit N-major B (transposing LDS reads) each block is costed at this share of its
+// rate: the time of the same problem with B K-major over its time N-major, measured on MI355X
+// (bf16; M x N x K = 4096^3, 4096 x 8192 x 2048, 2048 x 2048 x 8192, 1024 x 2048 x 8192,
+// 2048 x 6144 x 4096, 1024 x 4096 x 4096, 512 x 8192 x 2048; the 256x256 block 0.86-0.96,
+// 0.96 on the shapes it wins).
+static const double kBigNmajorShare[kNumBig] = {0.93, 0.91, 0.87, 0.87, 0.88, 0.79, 0.86};
 constexpr int kMenuSize = kBigCfg + kNumBig;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
@@ -225,17 +231,18 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   S::Math::store(acc, Cp, args.ldc, rows, cols, bias);
 }
 
-template <typename T, int BM, int BN, int SB>
+template <typename T, int BM, int BN, int SB, bool BKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void big_kernel(BmmArgs args) {
-  using Tile = BigTile<T, BM, BN, SB>;
+  using Tile = BigTile<T, BM, BN, SB, BKM>;
   __shared__ __attribute__((aligned(16))) char smem[Tile::SMEM_BYTES];
   const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
   if (t >= (uint32_t)args.total) return;
   const TileOrigin o = tile_origin(args, t, BM, BN);
   const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
+  // B K-major: column n at row n (stride ldb); N-major: column n at element n of each K row
   const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
-               (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
+               (o.b2 / (uint32_t)args.gB) * args.sB2 + (BKM ? o.n0 * args.ldb : o.n0);
   const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
   const int rows = rows64 < BM ? (int)rows64 : BM;
   const int cols = cols64 < BN ? (int)cols64 : BN;
@@ -301,8 +308,10 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   const bool grouped = a.grp != nullptr;
   const int forced = forced_cfg();
   if (forced == kSkinnyCfg && skinny_ok) return forced;
-  // 32-bit output offsets inside a 256-row tile
-  const bool big_ok = skinny_ok && dtype != BIOPS_F32 && a.ldc < (int64_t(1) << 23);
+  // Four-wave entries: the skinny conditions (direct loads, K-major B, plain rows, no SwiGLU),
+  // or the same with a 16-bit N-major B; 32-bit output offsets inside a 256-row tile.
+  const bool big_ok = (skinny_ok || (nmajor16 && !swiglu && !grouped)) && dtype != BIOPS_F32 &&
+                      a.ldc < (int64_t(1) << 23);
   if (forced >= kBigCfg && forced < kMenuSize && big_ok) return forced;
   if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
@@ -340,7 +349,8 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   if (big_ok && a.K >= 1024)
     for (int i = 0; i < kBigAutoCount; ++i) {
       const int64_t tiles = batch * cdiv(a.M, kBigBM[i]) * cdiv(a.N, kBigBN[i]);
-      const double cost = (double)cdiv(tiles, cus) * kBigBM[i] * kBigBN[i] / kBigRate[i];
+      const double rate = kBigRate[i] * (nmajor16 ? kBigNmajorShare[i] : 1.0);
+      const double cost = (double)cdiv(tiles, cus) * kBigBM[i] * kBigBN[i] / rate;
       if (cost < best_cost) { best_cost = cost; best = kBigCfg + i; }
     }
   if (best == 4 && prefer32) best = 6;
@@ -373,7 +383,7 @@ static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
   return launch_skinny_block<T, AR, 32>(a, stream);
 }
 
-template <typename T, int BM, int BN, int SB>
+template <typename T, int BM, int BN, int SB, bool BKM>
 static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   BmmArgs a = a0;
   a.tiles_m = cdiv(a.M, BM);
@@ -381,7 +391,7 @@ static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
-  hipLaunchKernelGGL((big_kernel<T, BM, BN, SB>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((big_kernel<T, BM, BN, SB, BKM>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
   return check_launch("big_kernel");
 }
 
@@ -466,13 +476,34 @@ static int launch_typed(const BmmArgs& a, bool b_kmajor, bool direct, int cfg, h
       case 10: return launch_layout<T, 10, EPI>(a, b_kmajor, direct, s);
       case 11: return launch_layout<T, 11, EPI>(a, b_kmajor, direct, s);
       case kSkinnyCfg: return launch_skinny<T>(a, s);
-      case kBigCfg: if constexpr (sizeof(T) == 2) return launch_big<T, 256, 256, 128>(a, s); break;
-      case kBigCfg + 1: if constexpr (sizeof(T) == 2) return launch_big<T, 256, 128, 128>(a, s); break;
-      case kBigCfg + 2: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 256, 128>(a, s); break;
-      case kBigCfg + 3: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 128, 128>(a, s); break;
-      case kBigCfg + 4: if constexpr (sizeof(T) == 2) return launch_big<T, 128, 64, 128>(a, s); break;
-      case kBigCfg + 5: if constexpr (sizeof(T) == 2) return launch_big<T, 64, 128, 128>(a, s); break;
-      case kBigCfg + 6: if constexpr (sizeof(T) == 2) return launch_big<T, 64, 64, 128>(a, s); break;
+      case kBigCfg:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 256, 256, 128, true>(a, s) : launch_big<T, 256, 256, 128, false>(a, s);
+        break;
+      case kBigCfg + 1:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 256, 128, 128, true>(a, s) : launch_big<T, 256, 128, 128, false>(a, s);
+        break;
+      case kBigCfg + 2:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 128, 256, 128, true>(a, s) : launch_big<T, 128, 256, 128, false>(a, s);
+        break;
+      case kBigCfg + 3:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 128, 128, 128, true>(a, s) : launch_big<T, 128, 128, 128, false>(a, s);
+        break;
+      case kBigCfg + 4:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 128, 64, 128, true>(a, s) : launch_big<T, 128, 64, 128, false>(a, s);
+        break;
+      case kBigCfg + 5:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 64, 128, 128, true>(a, s) : launch_big<T, 64, 128, 128, false>(a, s);
+        break;
+      case kBigCfg + 6:
+        if constexpr (sizeof(T) == 2)
+          return b_kmajor ? launch_big<T, 64, 64, 128, true>(a, s) : launch_big<T, 64, 64, 128, false>(a, s);
+        break;
       default: break;
     }
     return fail(BIOPS_ERR_ARG, "no kernel for tile config %d", cfg);

@@ -29,9 +29,13 @@
 
 namespace biops {
 
-template <typename T, int BM, int BN, int SB>
+// BKM: B K-major (an nn.Linear weight, [N, K] rows); otherwise N-major (row-major [K, N], N a
+// multiple of 8): a stage then holds 64 K rows of BN columns in the N-major layout of the table
+// entries (lds_off_n) and the B fragments come through the transposing LDS reads.
+template <typename T, int BM, int BN, int SB, bool BKM = true>
 struct BigTile {
   static_assert(sizeof(T) == 2, "16-bit operands");
+  static_assert(BKM || BN >= 64, "N-major stage rows of at least 8 chunks");
   static_assert(SB == 128, "whole K step per stage");
   static constexpr int THREADS = 256;
   static constexpr int WM = BM / 2, WN = BN / 2;
@@ -50,6 +54,7 @@ struct BigTile {
   static constexpr int A_LOADS = BM * CPR / THREADS;  // 16-byte chunks per thread per stage
   static constexpr int B_LOADS = BN * CPR / THREADS;
   static constexpr int LOADS = A_LOADS + B_LOADS;
+  static constexpr int CPR_N = BN / 8;            // 16-byte chunks per K row of an N-major stage
   static_assert(STAGES >= 2, "ring");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   static_assert(SMEM_BYTES <= LDS_MAX, "LDS");
@@ -58,6 +63,7 @@ struct BigTile {
   struct Frags {
     u32x4_t a[FM];
     u32x4_t b[FN];
+    u32x2_t lo[FN], hi[FN];  // N-major: the two transposing-read halves of b
   };
 
   __device__ static __forceinline__ int off(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
@@ -90,9 +96,36 @@ struct BigTile {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       f.a[i] = *reinterpret_cast<const u32x4_t*>(stage + off(wm * WM + i * 32 + lr, c));
+    if constexpr (BKM) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      f.b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + off(wn * WN + j * 32 + lr, c));
+      for (int j = 0; j < FN; ++j)
+        f.b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + off(wn * WN + j * 32 + lr, c));
+    } else {
+      // lane group g = lane / 16: columns 16 (g & 1) .. +15 of a 32-column block, K half g >> 1
+      // (the K values of chunk 2p + (lane >> 5), as on the K-major side); the reads are inline
+      // assembly, so that the compiler does not drain the global->LDS loads in flight before
+      // them, and ready() waits for them.
+      const int g = lane >> 4, s = lane & 15;
+      const int k = 16 * p + 8 * (g >> 1) + (s >> 2);
+      const int cb = 16 * (g & 1) + 4 * (s & 3);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const char* base = stage + LDS_A;
+        const int col = wn * WN + j * 32 + cb;
+        f.lo[j] = lds_read_tr16_asm(base + lds_off_n<CPR_N>(k, col));
+        f.hi[j] = lds_read_tr16_asm(base + lds_off_n<CPR_N>(k + 4, col));
+      }
+    }
+  }
+  // N-major: wait for the transposing reads of f and assemble the B fragments (no-op K-major).
+  __device__ static __forceinline__ void ready(Frags& f) {
+    if constexpr (!BKM) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        lds_wait_anchor(f.lo[j], f.hi[j]);
+        f.b[j] = u32x4_t{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
+      }
+    }
   }
 
   __device__ static __forceinline__ void mfmas(Acc (&acc)[FM][FN], const Frags& f) {
@@ -107,6 +140,7 @@ struct BigTile {
   // the next group waits for them (one read per two MFMAs left the last reads two MFMAs before
   // that wait).
   __device__ static __forceinline__ void interleave() {
+    if constexpr (!BKM) return;  // inline-assembly reads are not scheduling units
     constexpr int NR = FM + FN;
     constexpr int NG = (NR + 1) / 2;  // MFMAs followed by reads; NG <= NM for FM, FN >= 1
 #pragma unroll
@@ -125,6 +159,11 @@ struct BigTile {
   // rows (p < A_LOADS) or of the B columns, i.e. row r0 + 32p (r0 = t / 8), holding logical
   // chunk (t % 8) ^ ((r0 >> 1) & 7) -- the same chunk for every p, 32 being a multiple of 16.
   // Rows past the valid ones re-load the last valid row (their products are never stored).
+  // N-major B: slot s = t + 256 q of the B part is K row s / CPR_N, physical chunk
+  // t % CPR_N, i.e. K row k0 + (256 / CPR_N) q (k0 = t / CPR_N) holding logical chunk
+  // (t % CPR_N) ^ swz(k0) -- the same for every q (256 / CPR_N is a multiple of the swizzle's
+  // period); chunks past the tile's valid columns re-load its last whole chunk (N is a
+  // multiple of 8; their products are never stored).
   struct Src {
     const T* a;
     const T* b;
@@ -136,7 +175,14 @@ struct BigTile {
     const int t = threadIdx.x;
     const int r0 = t >> 3;
     const int c = (t & 7) ^ ((r0 >> 1) & 7);
-    return Src{A + c * VEC, B + c * VEC, lda, ldb, rows, cols, r0};
+    if constexpr (BKM) {
+      return Src{A + c * VEC, B + c * VEC, lda, ldb, rows, cols, r0};
+    } else {
+      const int k0 = t / CPR_N;
+      int col = VEC * ((t % CPR_N) ^ nmajor_swz<CPR_N>(k0));
+      if (col >= cols) col = cols - VEC;
+      return Src{A + c * VEC, B + (int64_t)k0 * ldb + col, lda, ldb, rows, cols, r0};
+    }
   }
   // Load p of this thread for the stage at K element k into ring slot `slot`.
   __device__ static __forceinline__ void issue_one(char* smem, const Src& src, int slot, int64_t k, int p) {
@@ -144,15 +190,17 @@ struct BigTile {
     // arithmetic instead of a vector value moved to a scalar register for every load (128x64
     // blocks at M=1024, N=2048, K=8192: 47.7 -> 44.6 us in a same-box A/B, same bits).
     const int wbase = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63);
-    const T* ptr;
+    const T* ptr;  // this load's 16 source bytes
     if (p < A_LOADS) {
       const int r = src.r0 + 32 * p;
-      ptr = src.a + (int64_t)(r < src.rows ? r : src.rows - 1) * src.lda;
-    } else {
+      ptr = src.a + (int64_t)(r < src.rows ? r : src.rows - 1) * src.lda + k;
+    } else if constexpr (BKM) {
       const int r = src.r0 + 32 * (p - A_LOADS);
-      ptr = src.b + (int64_t)(r < src.cols ? r : src.cols - 1) * src.ldb;
+      ptr = src.b + (int64_t)(r < src.cols ? r : src.cols - 1) * src.ldb + k;
+    } else {
+      ptr = src.b + (k + (int64_t)(THREADS / CPR_N) * (p - A_LOADS)) * src.ldb;  // K rows from k
     }
-    __builtin_amdgcn_global_load_lds((global_cvoid_t*)(ptr + k),
+    __builtin_amdgcn_global_load_lds((global_cvoid_t*)ptr,
                                      (lds_void_t*)(smem + slot * LDS_STAGE + (THREADS * p + wbase) * 16), 16, 0, 0);
   }
   // The MFMAs of one pair with the loads of a stage interleaved: MFMA q is followed by loads
@@ -183,7 +231,8 @@ struct BigTile {
   }
 
   // Full K loop of one tile into acc (zeroed here).  A: tile rows (rows valid), B: tile
-  // columns, K-major (cols valid), K a whole number of 128-byte steps.
+  // columns (cols valid; K-major rows, or N-major from the tile's first column), K a whole
+  // number of 128-byte steps.
   __device__ static __forceinline__ void mainloop(char* smem, Acc (&acc)[FM][FN], const T* A, int64_t lda,
                                                   int rows, const T* B, int64_t ldb, int cols, int64_t K) {
 #pragma unroll
@@ -212,8 +261,9 @@ struct BigTile {
       const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        const Frags& use = f[p & 1];
+        Frags& use = f[p & 1];
         Frags& next = f[(p + 1) & 1];
+        ready(use);
         if (p + 1 < P) {
           read_frags(st, p + 1, next);
           mfmas(acc, use);

@@ -205,13 +205,15 @@ def test_every_tile_entry_gives_identical_bits(tile_menu, dtype, m, k, n, layout
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-@pytest.mark.parametrize("broadcast", (False, True))
-def test_every_tile_entry_gives_identical_bits_bmm(tile_menu, dtype, broadcast):
-    """Batched products (a stride-0 expanded weight included) keep their bits on every entry,
-    the four-wave and skinny entries among them."""
+@pytest.mark.parametrize("layout", ("kmajor", "broadcast", "nmajor"))
+def test_every_tile_entry_gives_identical_bits_bmm(tile_menu, dtype, layout):
+    """Batched products (a stride-0 expanded weight and a row-major, N-major B included) keep
+    their bits on every entry, the four-wave and skinny entries among them."""
     a = gpu(randn(3, 300, 2048, seed=5500, dtype=dtype))
-    if broadcast:
+    if layout == "broadcast":
         b = gpu(randn(520, 2048, seed=5501, dtype=dtype)).t().unsqueeze(0).expand(3, -1, -1)
+    elif layout == "nmajor":
+        b = gpu(randn(3, 2048, 520, seed=5501, dtype=dtype))
     else:
         b = gpu(randn(3, 520, 2048, seed=5501, dtype=dtype)).transpose(1, 2)
     tile_menu.biops_set_gemm_tile(-1)
