@@ -172,6 +172,25 @@ def function(name: str):
     return getattr(load(), name)
 
 
+# Entry points with a CPython fast-call binding (_biops_fast, built beside libbiops.so): the
+# same C functions and arguments, without ctypes' per-argument conversions.
+_FAST = {"biops_gemm": "gemm", "biops_reduce": "reduce", "biops_softmax": "softmax"}
+
+
+def fast_function(name: str):
+    """``name`` through the fast-call module when it is built, else the ctypes binding.  The
+    library is loaded (and the GPU checked) first either way."""
+    lib = load()
+    alias = _FAST.get(name)
+    if alias is not None:
+        try:
+            from . import _biops_fast
+        except ImportError:
+            return getattr(lib, name)
+        return getattr(_biops_fast, alias)
+    return getattr(lib, name)
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load(require_gpu=False).biops_last_error().decode(errors="replace")

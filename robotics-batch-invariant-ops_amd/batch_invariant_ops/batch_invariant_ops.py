@@ -216,7 +216,7 @@ _gemm = None
 def _gemm_fn():
     global _gemm
     if _gemm is None:
-        _gemm = nat.function("biops_gemm")
+        _gemm = nat.fast_function("biops_gemm")
     return _gemm
 
 
@@ -250,7 +250,7 @@ _row_fns = {}
 def _row_fn(name):
     fn = _row_fns.get(name)
     if fn is None:
-        fn = _row_fns[name] = nat.function(name)
+        fn = _row_fns[name] = nat.fast_function(name)
     return fn
 
 

@@ -3,7 +3,9 @@
     python robotics-batch-invariant-ops_amd/build_lib.py [--jobs N]
 
 Each csrc/*.hip file is compiled to an object with hipcc for gfx950, then linked into
-batch_invariant_ops/libbiops.so next to the Python package that loads it.
+batch_invariant_ops/libbiops.so next to the Python package that loads it.  csrc/pyfast.c, a
+CPython fast-call binding of the most frequent entry points, is compiled with the host C
+compiler into batch_invariant_ops/_biops_fast (linked against libbiops.so beside it).
 """
 
 from __future__ import annotations
@@ -63,9 +65,28 @@ def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, OUT)
+    _build_fast()
     if verbose:
         print(f"built {OUT} from {len(sources)} sources", file=sys.stderr)
     return OUT
+
+
+def _build_fast() -> pathlib.Path:
+    """The CPython fast-call module next to libbiops.so (rpath $ORIGIN)."""
+    import sysconfig
+
+    out = OUT.parent / ("_biops_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_suffix(".tmp")
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no host C compiler for the fast-call module")
+    cmd = [cc, "-O2", "-shared", "-fPIC", f"-I{sysconfig.get_paths()['include']}", str(CSRC / "pyfast.c"),
+           f"-L{OUT.parent}", "-l:libbiops.so", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"fast-call module build failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -95,6 +95,33 @@ def test_conv_argument_rules_need_no_gpu():
     assert L.biops_conv_workspace_size(2, 2, 0, 2, 4, ptrs[0], 6, ptrs[1], ptrs[2], ptrs[3], ptrs[4], 3) == -1
 
 
+def test_fast_call_module_matches_the_ctypes_binding():
+    """The CPython fast-call module (built beside libbiops.so) reaches the same entry points
+    with the same arguments: the host checks give the same status codes; wrong argument counts
+    and non-integers raise."""
+    import importlib
+
+    fast = importlib.import_module("batch_invariant_ops._biops_fast")
+    L = lib()
+    null = None
+    for args in ((9, 4, 4, 4, 16, 4, 1, 16, 4, 1, null, 16, 4, 1, null),
+                 (2, -1, 4, 4, 16, 4, 1, 16, 4, 1, null, 16, 4, 1, null),
+                 (2, 4, 4, 4, 16, 4, 1, 16, 8, 8, null, 16, 4, 1, null),
+                 (2, 0, 4, 4, null, 4, 1, null, 4, 1, null, null, 4, 1, null)):
+        assert fast.gemm(*args) == L.biops_gemm(*args)
+    assert fast.softmax(2, 7, 4, 4, 16, 4, 16, 4, 0, null) == L.biops_softmax(2, 7, 4, 4, 16, 4, 16, 4, 0, null) == 3
+    assert fast.reduce(5, 2, 2, 1, 1, 1, 16, 1, 1, 1, 16, null) == 1
+    with pytest.raises(TypeError):
+        fast.gemm(2, 4, 4, 4)
+    with pytest.raises(TypeError):
+        fast.reduce(0, 2, 2, 4, 8, 1, "x", 8, 2, 1, 16, null)
+    if torch.cuda.is_available():
+        assert nat.fast_function("biops_gemm") is fast.gemm
+    else:  # the product path still insists on a GPU
+        with pytest.raises(RuntimeError, match="ROCm GPU"):
+            nat.fast_function("biops_gemm")
+
+
 def test_host_validation_needs_no_gpu():
     L = lib()
     null = None
