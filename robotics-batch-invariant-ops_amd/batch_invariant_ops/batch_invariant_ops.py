@@ -14,6 +14,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import math
+import threading
 from collections import namedtuple
 from typing import Any
 
@@ -656,27 +657,57 @@ def _offsets_on_host(cu_q, cu_kv):
     return host_q, np.ascontiguousarray(cu_kv.detach().cpu().numpy(), dtype=np.int64)
 
 
-def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal=None):
-    """The work list of biops_varlen_plan in pinned host memory (int64 tensor, ready for an
-    asynchronous upload), followed, when ``order_causal`` is a causal code, by the fused
-    kernel's tile order (biops_varlen_fused_order).  Returns (buffer, plan words, workspace
-    bytes); the buffer's numpy view starts with the plan."""
+class _VarlenStaging:
+    """The varlen work list's pinned host buffer and device buffer, one pair per (device,
+    stream), reused across calls.  The event recorded after each upload keeps the host buffer
+    untouched until that copy has run; a lock covers the write, the upload and the launch."""
+
+    _cache: dict = {}
+    _lock = threading.Lock()
+
+    def __init__(self, words, device):
+        self.host = torch.empty(words, dtype=torch.int64, pin_memory=True)
+        self.dev = torch.empty(words, dtype=torch.int64, device=device)
+        self.view = self.host.numpy()
+        self.event = torch.cuda.Event()
+
+    @classmethod
+    def get(cls, device, stream, words):
+        key = (device.index, stream)
+        st = cls._cache.get(key)
+        if st is None or st.view.size < words:
+            # a grown pair replaces the old one; torch's allocators keep the old blocks until the
+            # work queued on them has run
+            st = cls._cache[key] = cls(max(words, 4096, 2 * (st.view.size if st else 0)), device)
+        else:
+            st.event.synchronize()
+        return st
+
+
+def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal, out):
+    """The work list of biops_varlen_plan in ``out`` (int64 numpy array), followed, when
+    ``order_causal`` is a causal code, by the fused kernel's tile order
+    (biops_varlen_fused_order).  Returns (plan words, words used, workspace bytes)."""
     nseq = len(cu_q) - 1
-    lib = nat.load()
-    words = int(lib.biops_varlen_plan_len(nseq))
-    # at most total_q / 128 + nseq query tiles (each sequence adds at most one partial tile)
-    extra = int(cu_q[-1]) // 128 + nseq if order_causal is not None else 0
-    buf = torch.empty(words + extra, dtype=torch.int64, pin_memory=torch.cuda.is_available())
-    plan = buf.numpy()
-    ws_bytes = lib.biops_varlen_plan(
-        nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype), plan.ctypes.data
-    )
+    plan_fn = nat.fast_function("biops_varlen_plan")
+    words = int(nat.load().biops_varlen_plan_len(nseq))
+    ws_bytes = plan_fn(nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype),
+                       out.ctypes.data)
     if ws_bytes < 0:
-        raise ValueError(lib.biops_last_error().decode())
-    if order_causal is not None and plan[0] > 0:
-        if lib.biops_varlen_fused_order(plan.ctypes.data, order_causal, plan[words:].ctypes.data) < 0:
-            raise ValueError(lib.biops_last_error().decode())
-    return buf, words, ws_bytes
+        raise ValueError(nat.load().biops_last_error().decode())
+    used = words
+    if order_causal is not None and out[0] > 0:
+        n = nat.fast_function("biops_varlen_fused_order")(out.ctypes.data, order_causal, out[words:].ctypes.data)
+        if n < 0:
+            raise ValueError(nat.load().biops_last_error().decode())
+        used += int(n)
+    return words, used, ws_bytes
+
+
+def _varlen_words(nseq, total_q, fused):
+    """Upper bound of the plan (and tile order) words: at most total_q / 128 + nseq query tiles
+    (each sequence adds at most one partial tile)."""
+    return 8 + 8 * nseq + (total_q // 128 + nseq if fused else 0)
 
 
 def varlen_scaled_dot_product_attention_batch_invariant(
@@ -721,30 +752,16 @@ def varlen_scaled_dot_product_attention_batch_invariant(
     if query.dtype not in _FLOAT_DTYPES:
         raise ValueError(f"unsupported varlen attention dtype: {query.dtype}")
 
-    cu_q, cu_kv = _offsets_on_host(cumulative_seqlen_q, cumulative_seqlen_kv)
-    if cu_q.size == 0 or cu_q[0] != 0 or cu_kv[0] != 0:
-        raise ValueError("cumulative sequence lengths must start at zero")
-    if cu_q[-1] > query.shape[1] or cu_kv[-1] > key.shape[1]:
-        raise ValueError("cumulative sequence lengths exceed packed tensor size")
     nat.require_gpu_tensors(query, key, value)
-
     causal_name = getattr(causal_type, "name", None)
     if causal_name is None and causal_type is not None:
         causal_name = str(causal_type).rsplit(".", 1)[-1]
-    if is_causal and causal_name not in {"BottomRight", "TopLeft", None}:
-        q_lens, kv_lens = cu_q[1:] - cu_q[:-1], cu_kv[1:] - cu_kv[:-1]
-        if ((q_lens > 0) & (kv_lens > 0) & (q_lens != kv_lens)).any():
-            raise ValueError(f"causal type {causal_name!r} requires equal query and KV lengths")
-
     heads, kv_heads = query.shape[2], key.shape[2]
     head_dim, value_dim = query.shape[3], value.shape[3]
     out_shape = (1, query.shape[1], heads, value_dim)
-    if cu_q.size <= 1 or math.prod(out_shape) == 0:
-        # still reject decreasing offsets, as the planner does
-        if cu_q.size > 1 and ((cu_q[1:] < cu_q[:-1]).any() or (cu_kv[1:] < cu_kv[:-1]).any()):
-            raise ValueError("cumulative sequence lengths must be nondecreasing")
-        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
 
+    # Everything that does not depend on the offsets' values happens before the host waits for
+    # them (below), while the GPU still runs earlier work.
     def tokens_heads(x):
         return x if x.stride(3) == 1 or x.shape[3] <= 1 else x.contiguous()
 
@@ -754,46 +771,66 @@ def varlen_scaled_dot_product_attention_batch_invariant(
         causal = nat.CAUSAL_BOTTOM_RIGHT if causal_name == "BottomRight" else nat.CAUSAL_TOP_LEFT
     else:
         causal = nat.CAUSAL_NONE
-    # planner: validates the offsets (nondecreasing), drops empty sequences, and for the fused
-    # kernel appends the tile order (longest key range first)
-    buf, words, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype, causal if fused else None)
-    plan = buf.numpy()
-    if plan[0] == 0:
-        return torch.zeros(out_shape, dtype=value.dtype, device=value.device)
-    # The fused kernel writes every row of every sequence it computes (plan word 3 counts them
-    # per head); rows outside the sequences, or of a sequence with no keys, must read as zero.
-    every_row_written = fused and int(plan[3]) == heads * query.shape[1]
-    output = (torch.empty if every_row_written else torch.zeros)(out_shape, dtype=value.dtype, device=value.device)
-    scale_value = scale if scale is not None else 1.0 / math.sqrt(head_dim)
-    # one upload from pinned memory, without blocking the host (torch's pinned-memory cache keeps
-    # the block until the copy has run)
-    used = words + (int(plan[5]) if fused else 0)
-    dev = buf[:used].to(query.device, non_blocking=True)
-    if fused:
+    scale_value = float(scale if scale is not None else 1.0 / math.sqrt(head_dim))
+    output = torch.empty(out_shape, dtype=value.dtype, device=value.device)
+    stream = nat.stream_of(output)
+
+    cu_q, cu_kv = _offsets_on_host(cumulative_seqlen_q, cumulative_seqlen_kv)
+    if cu_q.size == 0 or cu_q[0] != 0 or cu_kv[0] != 0:
+        raise ValueError("cumulative sequence lengths must start at zero")
+    if cu_q[-1] > query.shape[1] or cu_kv[-1] > key.shape[1]:
+        raise ValueError("cumulative sequence lengths exceed packed tensor size")
+    if is_causal and causal_name not in {"BottomRight", "TopLeft", None}:
+        q_lens, kv_lens = cu_q[1:] - cu_q[:-1], cu_kv[1:] - cu_kv[:-1]
+        if ((q_lens > 0) & (kv_lens > 0) & (q_lens != kv_lens)).any():
+            raise ValueError(f"causal type {causal_name!r} requires equal query and KV lengths")
+    if cu_q.size <= 1 or math.prod(out_shape) == 0:
+        # still reject decreasing offsets, as the planner does
+        if cu_q.size > 1 and ((cu_q[1:] < cu_q[:-1]).any() or (cu_kv[1:] < cu_kv[:-1]).any()):
+            raise ValueError("cumulative sequence lengths must be nondecreasing")
+        return output.zero_()
+
+    nseq = cu_q.size - 1
+    with _VarlenStaging._lock:
+        st = _VarlenStaging.get(output.device, stream, _varlen_words(nseq, int(cu_q[-1]), fused))
+        # planner: validates the offsets (nondecreasing), drops empty sequences, and for the
+        # fused kernel appends the tile order (longest key range first)
+        words, used, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype,
+                                             causal if fused else None, st.view)
+        plan = st.view
+        if plan[0] == 0:
+            return output.zero_()
+        # The fused kernel writes every row of every sequence it computes (plan word 3 counts
+        # them per head); rows outside the sequences, or of a sequence with no keys, read zero.
+        if not (fused and int(plan[3]) == heads * query.shape[1]):
+            output.zero_()
+        dev = st.dev
+        dev[:used].copy_(st.host[:used], non_blocking=True)
+        st.event.record()
+        if fused:
+            rc = nat.fast_function("biops_varlen_sdpa_fused")(
+                nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
+                q.data_ptr(), q.stride(1), q.stride(2),
+                k.data_ptr(), k.stride(1), k.stride(2),
+                v.data_ptr(), v.stride(1), v.stride(2),
+                output.data_ptr(), output.stride(1), output.stride(2),
+                dev.data_ptr(), plan.ctypes.data, dev.data_ptr() + 8 * words, causal, scale_value, stream,
+            )
+            nat.check(rc, "biops_varlen_sdpa_fused")
+            return output
+        workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
         nat.call(
-            "biops_varlen_sdpa_fused",
+            "biops_varlen_sdpa",
             nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
             q.data_ptr(), q.stride(1), q.stride(2),
             k.data_ptr(), k.stride(1), k.stride(2),
             v.data_ptr(), v.stride(1), v.stride(2),
             output.data_ptr(), output.stride(1), output.stride(2),
-            dev.data_ptr(), plan.ctypes.data, dev[words:].data_ptr(), causal, float(scale_value),
-            nat.stream_of(output),
+            dev.data_ptr(), plan.ctypes.data, causal, scale_value,
+            workspace.data_ptr(), workspace.numel(),
+            stream,
         )
         return output
-    workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
-    nat.call(
-        "biops_varlen_sdpa",
-        nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
-        q.data_ptr(), q.stride(1), q.stride(2),
-        k.data_ptr(), k.stride(1), k.stride(2),
-        v.data_ptr(), v.stride(1), v.stride(2),
-        output.data_ptr(), output.stride(1), output.stride(2),
-        dev.data_ptr(), plan.ctypes.data, causal, float(scale_value),
-        workspace.data_ptr(), workspace.numel(),
-        nat.stream_of(output),
-    )
-    return output
 
 
 # ---------------------------------------------------------------- convolutions ----

@@ -1,7 +1,8 @@
 /* Fast-call CPython binding of the library's most frequent entry points (GEMM, row
- * reductions, softmax): the same C ABI as the ctypes binding, without the per-argument ctypes
- * conversions.  Python integers are taken as int64 values or addresses (None is a null
- * pointer); each function returns the entry point's status code.  Optional: the Python package
+ * reductions, softmax, the varlen planner and fused varlen attention): the same C ABI as the
+ * ctypes binding, without the per-argument ctypes conversions.  Python integers are taken as
+ * int64 values or addresses (None is a null pointer), Python floats as float; each function
+ * returns the entry point's result.  Optional: the Python package
  * falls back to ctypes when this module is absent.  Linked against libbiops.so in the same
  * directory. */
 #define PY_SSIZE_T_CLEAN
@@ -25,15 +26,25 @@ static int as_ptr(PyObject* o, void** p) {
   return !(*p == NULL && PyErr_Occurred());
 }
 
-/* Converts args[i] by kind: 'l' int64, 'p' pointer. */
-static int parse(PyObject* const* args, Py_ssize_t nargs, const char* kinds, int64_t* iv, void** pv) {
+static int as_f32(PyObject* o, float* v) {
+  const double d = PyFloat_AsDouble(o);
+  *v = (float)d;
+  return !(d == -1.0 && PyErr_Occurred());
+}
+
+/* Converts args[i] by kind: 'l' int64 (iv), 'p' pointer (pv), 'f' float (fv). */
+static int parse(PyObject* const* args, Py_ssize_t nargs, const char* kinds, int64_t* iv, void** pv, float* fv) {
   Py_ssize_t n = (Py_ssize_t)strlen(kinds);
   if (nargs != n) {
     PyErr_Format(PyExc_TypeError, "expected %zd arguments, got %zd", n, nargs);
     return 0;
   }
   for (Py_ssize_t i = 0; i < n; ++i) {
-    if (kinds[i] == 'p' ? !as_ptr(args[i], &pv[i]) : !as_i64(args[i], &iv[i])) return 0;
+    int ok;
+    if (kinds[i] == 'p') ok = as_ptr(args[i], &pv[i]);
+    else if (kinds[i] == 'f') ok = as_f32(args[i], &fv[i]);
+    else ok = as_i64(args[i], &iv[i]);
+    if (!ok) return 0;
   }
   return 1;
 }
@@ -43,7 +54,7 @@ static PyObject* fast_gemm(PyObject* self, PyObject* const* args, Py_ssize_t nar
   int64_t iv[15];
   void* pv[15];
   (void)self;
-  if (!parse(args, nargs, "llllpllpllppllp", iv, pv)) return NULL;
+  if (!parse(args, nargs, "llllpllpllppllp", iv, pv, NULL)) return NULL;
   return PyLong_FromLong(biops_gemm((int)iv[0], iv[1], iv[2], iv[3], pv[4], iv[5], iv[6], pv[7], iv[8], iv[9],
                                     pv[10], pv[11], iv[12], iv[13], pv[14]));
 }
@@ -53,7 +64,7 @@ static PyObject* fast_reduce(PyObject* self, PyObject* const* args, Py_ssize_t n
   int64_t iv[12];
   void* pv[12];
   (void)self;
-  if (!parse(args, nargs, "llllllplllpp", iv, pv)) return NULL;
+  if (!parse(args, nargs, "llllllplllpp", iv, pv, NULL)) return NULL;
   return PyLong_FromLong(biops_reduce((int)iv[0], (int)iv[1], (int)iv[2], iv[3], iv[4], iv[5], pv[6], iv[7],
                                       iv[8], iv[9], pv[10], pv[11]));
 }
@@ -63,15 +74,53 @@ static PyObject* fast_softmax(PyObject* self, PyObject* const* args, Py_ssize_t 
   int64_t iv[10];
   void* pv[10];
   (void)self;
-  if (!parse(args, nargs, "llllplpllp", iv, pv)) return NULL;
+  if (!parse(args, nargs, "llllplpllp", iv, pv, NULL)) return NULL;
   return PyLong_FromLong(biops_softmax((int)iv[0], (int)iv[1], iv[2], iv[3], pv[4], iv[5], pv[6], iv[7],
                                        (int)iv[8], pv[9]));
+}
+
+/* varlen_plan(nseq, cu_q, cu_kv, hq, dv, dtype, plan) -> workspace bytes or < 0 */
+static PyObject* fast_varlen_plan(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[7];
+  void* pv[7];
+  (void)self;
+  if (!parse(args, nargs, "lpplllp", iv, pv, NULL)) return NULL;
+  return PyLong_FromLongLong(biops_varlen_plan(iv[0], (const int64_t*)pv[1], (const int64_t*)pv[2], iv[3], iv[4],
+                                               (int)iv[5], (int64_t*)pv[6]));
+}
+
+/* varlen_fused_order(plan, causal, order) -> entries or < 0 */
+static PyObject* fast_varlen_fused_order(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[3];
+  void* pv[3];
+  (void)self;
+  if (!parse(args, nargs, "plp", iv, pv, NULL)) return NULL;
+  return PyLong_FromLongLong(biops_varlen_fused_order((const int64_t*)pv[0], (int)iv[1], (int64_t*)pv[2]));
+}
+
+/* varlen_sdpa_fused(dtype, hq, hkv, d, dv, q, sq_t, sq_h, k, sk_t, sk_h, v, sv_t, sv_h, out,
+ *                   so_t, so_h, dplan, hplan, dorder, causal, scale, stream) */
+static PyObject* fast_varlen_sdpa_fused(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[23];
+  void* pv[23];
+  float fv[23];
+  (void)self;
+  if (!parse(args, nargs, "lllllpllpllpllpllppplfp", iv, pv, fv)) return NULL;
+  return PyLong_FromLong(biops_varlen_sdpa_fused((int)iv[0], iv[1], iv[2], iv[3], iv[4], pv[5], iv[6], iv[7], pv[8],
+                                                 iv[9], iv[10], pv[11], iv[12], iv[13], pv[14], iv[15], iv[16],
+                                                 (const int64_t*)pv[17], (const int64_t*)pv[18],
+                                                 (const int64_t*)pv[19], (int)iv[20], fv[21], pv[22]));
 }
 
 static PyMethodDef kMethods[] = {
     {"gemm", (PyCFunction)(void (*)(void))fast_gemm, METH_FASTCALL, "biops_gemm"},
     {"reduce", (PyCFunction)(void (*)(void))fast_reduce, METH_FASTCALL, "biops_reduce"},
     {"softmax", (PyCFunction)(void (*)(void))fast_softmax, METH_FASTCALL, "biops_softmax"},
+    {"varlen_plan", (PyCFunction)(void (*)(void))fast_varlen_plan, METH_FASTCALL, "biops_varlen_plan"},
+    {"varlen_fused_order", (PyCFunction)(void (*)(void))fast_varlen_fused_order, METH_FASTCALL,
+     "biops_varlen_fused_order"},
+    {"varlen_sdpa_fused", (PyCFunction)(void (*)(void))fast_varlen_sdpa_fused, METH_FASTCALL,
+     "biops_varlen_sdpa_fused"},
     {NULL, NULL, 0, NULL},
 };
 

@@ -115,6 +115,20 @@ def test_fast_call_module_matches_the_ctypes_binding():
         fast.gemm(2, 4, 4, 4)
     with pytest.raises(TypeError):
         fast.reduce(0, 2, 2, 4, 8, 1, "x", 8, 2, 1, 16, null)
+    # the varlen planner and tile order give the ctypes binding's words
+    cu_q = np.array([0, 5, 5, 305, 435], dtype=np.int64)
+    cu_k = np.array([0, 7, 11, 11, 140], dtype=np.int64)
+    a, b = np.zeros(64, dtype=np.int64), np.ones(64, dtype=np.int64)
+    assert (fast.varlen_plan(4, cu_q.ctypes.data, cu_k.ctypes.data, 4, 24, 2, a.ctypes.data)
+            == L.biops_varlen_plan(4, cu_q.ctypes.data, cu_k.ctypes.data, 4, 24, 2, b.ctypes.data) > 0)
+    words = 8 + 8 * int(a[0])  # header and the kept sequences' entries
+    assert a[0] == 2 and (a[:words] == b[:words]).all()
+    oa, ob = np.zeros(3, dtype=np.int64), np.ones(3, dtype=np.int64)
+    assert fast.varlen_fused_order(a.ctypes.data, 2, oa.ctypes.data) == L.biops_varlen_fused_order(
+        a.ctypes.data, 2, ob.ctypes.data) == 3
+    assert (oa == ob).all()
+    args = (2, 8, 2, 64, 64) + (16, 8, 64) * 4 + (null, null, null, 2, 0.125, null)
+    assert fast.varlen_sdpa_fused(*args) == L.biops_varlen_sdpa_fused(*args) != 0  # null plan
     if torch.cuda.is_available():
         assert nat.fast_function("biops_gemm") is fast.gemm
     else:  # the product path still insists on a GPU
