@@ -175,7 +175,7 @@ def function(name: str):
 # Entry points with a CPython fast-call binding (_biops_fast, built beside libbiops.so): the
 # same C functions and arguments, without ctypes' per-argument conversions.
 _FAST = {"biops_gemm": "gemm", "biops_reduce": "reduce", "biops_softmax": "softmax",
-         "biops_varlen_plan": "varlen_plan", "biops_varlen_fused_order": "varlen_fused_order",
+         "biops_sdpa_fused": "sdpa_fused", "biops_varlen_plan": "varlen_plan", "biops_varlen_fused_order": "varlen_fused_order",
          "biops_varlen_sdpa_fused": "varlen_sdpa_fused"}
 
 

@@ -617,8 +617,7 @@ def scaled_dot_product_attention_batch_invariant(
     if fused and mask4 is not None:
         fused = bool(nat.load().biops_attention_fused_mask_ok(mask4.data_ptr(), mask_code, Lk, *mask4.stride()))
     if fused:
-        nat.call(
-            "biops_sdpa_fused",
+        rc = nat.fast_function("biops_sdpa_fused")(
             nat.dtype_code(query.dtype), B, Hq, Hkv, Lq, Lk, D, Dv,
             q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2),
             k4.data_ptr(), k4.stride(0), k4.stride(1), k4.stride(2),
@@ -627,6 +626,7 @@ def scaled_dot_product_attention_batch_invariant(
             *(mask4.stride() if mask4 is not None else (0, 0, 0, 0)),
             causal_code, float(scale_value), out.data_ptr(), nat.stream_of(out),
         )
+        nat.check(rc, "biops_sdpa_fused")
         return out.reshape(*leading, Lq, Dv)
     ws_bytes = nat.load().biops_sdpa_workspace_size(nat.dtype_code(query.dtype), B, Hq, Lq, Lk)
     workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=query.device)

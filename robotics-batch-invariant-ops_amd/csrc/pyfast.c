@@ -1,6 +1,6 @@
 /* Fast-call CPython binding of the library's most frequent entry points (GEMM, row
- * reductions, softmax, the varlen planner and fused varlen attention): the same C ABI as the
- * ctypes binding, without the per-argument ctypes conversions.  Python integers are taken as
+ * reductions, softmax, fused attention, the varlen planner and fused varlen attention): the
+ * same C ABI as the ctypes binding, without the per-argument ctypes conversions.  Python integers are taken as
  * int64 values or addresses (None is a null pointer), Python floats as float; each function
  * returns the entry point's result.  Optional: the Python package
  * falls back to ctypes when this module is absent.  Linked against libbiops.so in the same
@@ -112,10 +112,25 @@ static PyObject* fast_varlen_sdpa_fused(PyObject* self, PyObject* const* args, P
                                                  (const int64_t*)pv[19], (int)iv[20], fv[21], pv[22]));
 }
 
+/* sdpa_fused(dtype, batch, hq, hkv, lq, lk, d, dv, q, sqB, sqH, sqL, k, skB, skH, skL, v, svB,
+ *            svH, svL, mask, mask_dtype, mB, mH, mI, mJ, causal, scale, out, stream) */
+static PyObject* fast_sdpa_fused(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[30];
+  void* pv[30];
+  float fv[30];
+  (void)self;
+  if (!parse(args, nargs, "llllllllplllplllplllpllllllfpp", iv, pv, fv)) return NULL;
+  return PyLong_FromLong(biops_sdpa_fused((int)iv[0], iv[1], iv[2], iv[3], iv[4], iv[5], iv[6], iv[7], pv[8], iv[9],
+                                          iv[10], iv[11], pv[12], iv[13], iv[14], iv[15], pv[16], iv[17], iv[18],
+                                          iv[19], pv[20], (int)iv[21], iv[22], iv[23], iv[24], iv[25], (int)iv[26],
+                                          fv[27], pv[28], pv[29]));
+}
+
 static PyMethodDef kMethods[] = {
     {"gemm", (PyCFunction)(void (*)(void))fast_gemm, METH_FASTCALL, "biops_gemm"},
     {"reduce", (PyCFunction)(void (*)(void))fast_reduce, METH_FASTCALL, "biops_reduce"},
     {"softmax", (PyCFunction)(void (*)(void))fast_softmax, METH_FASTCALL, "biops_softmax"},
+    {"sdpa_fused", (PyCFunction)(void (*)(void))fast_sdpa_fused, METH_FASTCALL, "biops_sdpa_fused"},
     {"varlen_plan", (PyCFunction)(void (*)(void))fast_varlen_plan, METH_FASTCALL, "biops_varlen_plan"},
     {"varlen_fused_order", (PyCFunction)(void (*)(void))fast_varlen_fused_order, METH_FASTCALL,
      "biops_varlen_fused_order"},

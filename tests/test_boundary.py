@@ -129,6 +129,19 @@ def test_fast_call_module_matches_the_ctypes_binding():
     assert (oa == ob).all()
     args = (2, 8, 2, 64, 64) + (16, 8, 64) * 4 + (null, null, null, 2, 0.125, null)
     assert fast.varlen_sdpa_fused(*args) == L.biops_varlen_sdpa_fused(*args) != 0  # null plan
+    # dense fused attention: fp32 outside the envelope, an odd row stride, mask with causal
+    qkv = (256, 0, 0, 128) * 3
+    for args in ((nat.F32, 1, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null),
+                 (nat.BF16, 1, 1, 1, 4, 4, 128, 128, 256, 0, 0, 130) + qkv[4:]
+                 + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null),
+                 (nat.BF16, 1, 1, 1, 4, 4, 128, 128) + qkv + (256, nat.BOOL, 0, 0, 4, 1, 1, 1.0, 256, null),
+                 (nat.BF16, 0, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null)):
+        assert fast.sdpa_fused(*args) == L.biops_sdpa_fused(*args)
+    assert [fast.sdpa_fused(*a) for a in (
+        (nat.F32, 1, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null),
+        (nat.BF16, 0, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null))] == [3, 0]
+    with pytest.raises(TypeError):
+        fast.sdpa_fused(*((nat.BF16, 1, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, "x", 256, null)))
     if torch.cuda.is_available():
         assert nat.fast_function("biops_gemm") is fast.gemm
     else:  # the product path still insists on a GPU
