@@ -19,6 +19,13 @@
 // The compiler waits for all outstanding LDS reads before an MFMA that needs one (the global
 // -> LDS loads make its LDS counter out of order), so each group starts with one wait and its
 // MFMAs only read fragments loaded during the previous group.
+// K-major blocks from 128 x 128 up take two pairs per group instead (group A: pairs 0, 1 with
+// the reads of pairs 2, 3; group B: wait, barrier, the reads of pairs 0, 1 of stage h+1, pairs
+// 2, 3 with the refill), so that a read has two pairs of MFMAs to land, not one.  Measured on
+// MI355X in a same-box A/B (bitwise-identical outputs): 256 x 256 at M = 4096, N = 8192,
+// K = 2048 112.0 -> 110.4 us and K = 8192 379 -> 370 us; 256 x 128 at 4096 x 2048 x 8192
+// 109.9 -> 106.6 us; 128 x 128 at 2048 x 2048 x 8192 64.7 -> 63.0 us; 128 x 256 at
+// 2048 x 8192 x 2048 67.7 -> 64.6 us.
 //
 // LDS stage layout: A rows (BM x 128 bytes) then B columns (BN x 128 bytes).  A 16-byte read
 // serves 16 lanes per clock from a 256-byte window, so 16 consecutive rows reading the same
@@ -230,6 +237,59 @@ struct BigTile {
     }
   }
 
+  // Two pairs per group when a group's reads fit after the first pair's first MFMAs (two reads
+  // after each).
+  static constexpr bool TWO_PAIR = BKM && (FM + FN) <= NM;
+  struct Frags2 {
+    Frags f[2];
+  };
+  __device__ static __forceinline__ void read2(const char* stage, int p0, Frags2& g) {
+    read_frags(stage, p0, g.f[0]);
+    read_frags(stage, p0 + 1, g.f[1]);
+  }
+  // The 2 (FM + FN) reads of a group, two after each of its first MFMAs, then the rest of the
+  // MFMAS MFMAs this pattern covers.
+  template <int MFMAS>
+  __device__ static __forceinline__ void interleave2() {
+    constexpr int NR = 2 * (FM + FN);
+    static_assert(NR / 2 <= MFMAS, "reads after the MFMAs");
+#pragma unroll
+    for (int i = 0; i < NR / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
+    if constexpr (MFMAS > NR / 2) __builtin_amdgcn_sched_group_barrier(0x008, MFMAS - NR / 2, 0);
+  }
+  __device__ static __forceinline__ void mainloop_two_pair(char* smem, Acc (&acc)[FM][FN], const Src& src,
+                                                           int64_t H) {
+    auto stage_k = [&](int64_t h) { return (h < H ? h : H - 1) * STAGE_ELEMS; };
+    Frags2 F[2];
+    read2(smem, 0, F[0]);
+    int cur = 0;
+    for (int64_t h = 0; h < H; ++h) {
+      const char* st = smem + cur * LDS_STAGE;
+      const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+      // group A: pairs 0, 1 (read during the previous group B) with the reads of pairs 2, 3
+      read2(st, 2, F[1]);
+      mfmas(acc, F[0].f[0]);
+      mfmas(acc, F[0].f[1]);
+      interleave2<2 * NM>();
+      __builtin_amdgcn_sched_barrier(0);
+      // group B: stage h+1 landed and published (all of stage h has been read), its pairs 0, 1
+      // read, then pairs 2, 3 with the refill of slot h by stage h+STAGES
+      wait_loads<(STAGES - 2) * LOADS>();
+      lds_barrier();
+      read2(smem + nxt * LDS_STAGE, 0, F[0]);
+      mfmas(acc, F[1].f[0]);
+      interleave2<NM>();
+      mfmas_loads(acc, F[1].f[1], smem, src, cur, stage_k(h + STAGES));
+      __builtin_amdgcn_sched_barrier(0);
+      cur = nxt;
+    }
+    wait_loads<0>();
+    lds_barrier();  // the ring is idle
+  }
+
   // Full K loop of one tile into acc (zeroed here).  A: tile rows (rows valid), B: tile
   // columns (cols valid; K-major rows, or N-major from the tile's first column), K a whole
   // number of 128-byte steps.
@@ -253,6 +313,10 @@ struct BigTile {
       for (int p = 0; p < LOADS; ++p) issue_one(smem, src, s, stage_k(s), p);
     wait_loads<(STAGES - 1) * LOADS>();  // stage 0 landed
     lds_barrier();
+    if constexpr (TWO_PAIR) {
+      mainloop_two_pair(smem, acc, src, H);
+      return;
+    }
     Frags f[2];
     read_frags(smem, 0, f[0]);
     int cur = 0;  // ring slot of stage h
