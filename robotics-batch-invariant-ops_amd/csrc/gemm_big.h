@@ -2,7 +2,12 @@
 // (BM/2) x (BN/2) wave tile whose fp32 accumulators live in the accumulation registers (one
 // wavefront per SIMD, 16 independent 32x32 accumulators at 256 x 256, one at 64 x 64).  Blocks
 // from 256 x 256 down to 64 x 64; the ring takes as many stages as 160 KiB of LDS holds (2 at
-// 256 x 256, 10 at 64 x 64), so one workgroup owns a compute unit.
+// 256 x 256, 10 at 64 x 64), except that K-major 128 x 128 blocks keep 3 and 128 x 64 / 64 x 128
+// blocks 4 (fewer in flight measured faster: same-box A/B in alternating order, 128 x 128 at
+// M = 2048, N = 2048, K = 8192 63.8 -> 62.4 us, 512 x 8192 x 2048 22.0 -> 21.2 us; 64 x 128 at
+// 256 x 8192 x 2048 16.0 -> 15.2 us, 1024 x 2048 x 8192 43.8 -> 43.3 us; 128 x 64 at
+// 512 x 8192 x 2048 28.2 -> 27.3 us; two stages are slower everywhere); one workgroup owns a
+// compute unit.
 //
 // Same arithmetic as every other tile entry (gemm_core.h): 128-byte K steps in order, chunk
 // pairs q = 0..3 in order inside a step.  A stage of the LDS ring holds one K step (SB = 128
@@ -22,10 +27,10 @@
 // K-major blocks from 128 x 128 up take two pairs per group instead (group A: pairs 0, 1 with
 // the reads of pairs 2, 3; group B: wait, barrier, the reads of pairs 0, 1 of stage h+1, pairs
 // 2, 3 with the refill), so that a read has two pairs of MFMAs to land, not one.  Measured on
-// MI355X in a same-box A/B (bitwise-identical outputs): 256 x 256 at M = 4096, N = 8192,
-// K = 2048 112.0 -> 110.4 us and K = 8192 379 -> 370 us; 256 x 128 at 4096 x 2048 x 8192
-// 109.9 -> 106.6 us; 128 x 128 at 2048 x 2048 x 8192 64.7 -> 63.0 us; 128 x 256 at
-// 2048 x 8192 x 2048 67.7 -> 64.6 us.
+// MI355X (same-box A/B, the two kernels timed in alternating order, bitwise-identical outputs):
+// 256 x 256 at M = 4096, N = 8192, K = 2048 114.5 -> 113.0 us and K = 8192 378.2 -> 373.8 us;
+// 256 x 128 at 4096 x 2048 x 8192 110.1 -> 107.5 us; 128 x 128 at 2048 x 2048 x 8192
+// 63.8 -> 62.6 us; 128 x 256 at 2048 x 8192 x 2048 70.1 -> 69.0 us.
 //
 // LDS stage layout: A rows (BM x 128 bytes) then B columns (BN x 128 bytes).  A 16-byte read
 // serves 16 lanes per clock from a 256-byte window, so 16 consecutive rows reading the same
@@ -55,7 +60,8 @@ struct BigTile {
   static constexpr int LDS_A = BM * SB;
   static constexpr int LDS_STAGE = (BM + BN) * SB;
   static constexpr int LDS_MAX = 160 * 1024;
-  static constexpr int STAGES = LDS_MAX / LDS_STAGE;
+  static constexpr int MAX_STAGES = LDS_MAX / LDS_STAGE;
+  static constexpr int STAGES = !BKM ? MAX_STAGES : BM * BN == 128 * 128 ? 3 : BM * BN == 128 * 64 ? 4 : MAX_STAGES;
   static constexpr int RING = STAGES * LDS_STAGE;
   static constexpr int SMEM_BYTES = RING;
   static constexpr int A_LOADS = BM * CPR / THREADS;  // 16-byte chunks per thread per stage
