@@ -193,6 +193,18 @@ def fast_function(name: str):
     return getattr(lib, name)
 
 
+def fast_copy_h2d():
+    """``copy_h2d(dst, src, bytes, stream)`` (hipMemcpyAsync host to device, returns the HIP
+    status) from the fast-call module, or None when the module is not built.  The library is
+    loaded (and the GPU checked) first."""
+    load()
+    try:
+        from . import _biops_fast
+    except ImportError:
+        return None
+    return _biops_fast.copy_h2d
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load(require_gpu=False).biops_last_error().decode(errors="replace")

@@ -245,13 +245,14 @@ def bmm_batch_invariant(a, b):
 
 
 # --------------------------------------------------------------- row reductions ----
-_row_fns = {}
+_fast_fns = {}
 
 
-def _row_fn(name):
-    fn = _row_fns.get(name)
+def _fast_fn(name):
+    """nat.fast_function(name), looked up once."""
+    fn = _fast_fns.get(name)
     if fn is None:
-        fn = _row_fns[name] = nat.fast_function(name)
+        fn = _fast_fns[name] = nat.fast_function(name)
     return fn
 
 
@@ -274,7 +275,7 @@ def _reduce_last_fast(op, input, n, keepdim):
     shape = input.shape
     out = torch.empty((*shape[:-1], 1) if keepdim else shape[:-1], dtype=input.dtype, device=input.device)
     code = nat.DIRECT_DTYPES[input.dtype]
-    rc = _row_fn("biops_reduce")(op, code, code, input.numel() // n, n, 1, input.data_ptr(), n, 1, 1,
+    rc = _fast_fn("biops_reduce")(op, code, code, input.numel() // n, n, 1, input.data_ptr(), n, 1, 1,
                                  out.data_ptr(), nat.stream_of(out))
     if rc:
         nat.check(rc, "biops_reduce")
@@ -294,7 +295,7 @@ def _softmax_impl(input, dim, out_dtype, is_log):
     n = _last_dim_fast(input, dim)
     if n and out_dtype in nat.DIRECT_DTYPES:
         out = torch.empty(input.shape, dtype=out_dtype, device=input.device)
-        rc = _row_fn("biops_softmax")(nat.DIRECT_DTYPES[input.dtype], nat.DIRECT_DTYPES[out_dtype],
+        rc = _fast_fn("biops_softmax")(nat.DIRECT_DTYPES[input.dtype], nat.DIRECT_DTYPES[out_dtype],
                                       input.numel() // n, n, input.data_ptr(), n, out.data_ptr(), n,
                                       int(is_log), nat.stream_of(out))
         if rc:
@@ -617,7 +618,7 @@ def scaled_dot_product_attention_batch_invariant(
     if fused and mask4 is not None:
         fused = bool(nat.load().biops_attention_fused_mask_ok(mask4.data_ptr(), mask_code, Lk, *mask4.stride()))
     if fused:
-        rc = nat.fast_function("biops_sdpa_fused")(
+        rc = _fast_fn("biops_sdpa_fused")(
             nat.dtype_code(query.dtype), B, Hq, Hkv, Lq, Lk, D, Dv,
             q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2),
             k4.data_ptr(), k4.stride(0), k4.stride(1), k4.stride(2),
@@ -664,6 +665,7 @@ class _VarlenStaging:
 
     _cache: dict = {}
     _lock = threading.Lock()
+    _h2d = None  # the fast-call module's host-to-device copy, False without the module
 
     def __init__(self, words, device):
         self.host = torch.empty(words, dtype=torch.int64, pin_memory=True)
@@ -675,13 +677,27 @@ class _VarlenStaging:
     def get(cls, device, stream, words):
         key = (device.index, stream)
         st = cls._cache.get(key)
+        if st is not None:
+            st.event.synchronize()  # the last upload from the host buffer has run
         if st is None or st.view.size < words:
-            # a grown pair replaces the old one; torch's allocators keep the old blocks until the
-            # work queued on them has run
+            # a grown pair replaces the old one (the device buffer goes back to torch's stream-
+            # ordered allocator; the work queued on it runs first)
             st = cls._cache[key] = cls(max(words, 4096, 2 * (st.view.size if st else 0)), device)
-        else:
-            st.event.synchronize()
         return st
+
+    def upload(self, used, stream):
+        """The first ``used`` words of the host buffer to the device buffer, on ``stream``,
+        then the event that guards the host buffer."""
+        copy = nat.fast_copy_h2d() if _VarlenStaging._h2d is None else _VarlenStaging._h2d
+        if copy:
+            _VarlenStaging._h2d = copy
+            rc = copy(self.dev.data_ptr(), self.host.data_ptr(), 8 * used, stream)
+            if rc != 0:
+                raise RuntimeError(f"hipMemcpyAsync of the varlen work list failed ({rc})")
+        else:
+            _VarlenStaging._h2d = False
+            self.dev[:used].copy_(self.host[:used], non_blocking=True)
+        self.event.record()
 
 
 def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal, out):
@@ -689,7 +705,7 @@ def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal, out):
     ``order_causal`` is a causal code, by the fused kernel's tile order
     (biops_varlen_fused_order).  Returns (plan words, words used, workspace bytes)."""
     nseq = len(cu_q) - 1
-    plan_fn = nat.fast_function("biops_varlen_plan")
+    plan_fn = _fast_fn("biops_varlen_plan")
     words = int(nat.load().biops_varlen_plan_len(nseq))
     ws_bytes = plan_fn(nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype),
                        out.ctypes.data)
@@ -697,7 +713,7 @@ def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal, out):
         raise ValueError(nat.load().biops_last_error().decode())
     used = words
     if order_causal is not None and out[0] > 0:
-        n = nat.fast_function("biops_varlen_fused_order")(out.ctypes.data, order_causal, out[words:].ctypes.data)
+        n = _fast_fn("biops_varlen_fused_order")(out.ctypes.data, order_causal, out.ctypes.data + 8 * words)
         if n < 0:
             raise ValueError(nat.load().biops_last_error().decode())
         used += int(n)
@@ -805,10 +821,9 @@ def varlen_scaled_dot_product_attention_batch_invariant(
         if not (fused and int(plan[3]) == heads * query.shape[1]):
             output.zero_()
         dev = st.dev
-        dev[:used].copy_(st.host[:used], non_blocking=True)
-        st.event.record()
+        st.upload(used, stream)
         if fused:
-            rc = nat.fast_function("biops_varlen_sdpa_fused")(
+            rc = _fast_fn("biops_varlen_sdpa_fused")(
                 nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
                 q.data_ptr(), q.stride(1), q.stride(2),
                 k.data_ptr(), k.stride(1), k.stride(2),

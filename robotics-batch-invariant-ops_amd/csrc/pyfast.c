@@ -1,6 +1,7 @@
 /* Fast-call CPython binding of the library's most frequent entry points (GEMM, row
- * reductions, softmax, fused attention, the varlen planner and fused varlen attention): the
- * same C ABI as the ctypes binding, without the per-argument ctypes conversions.  Python integers are taken as
+ * reductions, softmax, fused attention, the varlen planner and fused varlen attention) and of
+ * the host-to-device copy of the varlen work list: the same C ABI as the ctypes binding,
+ * without the per-argument ctypes conversions.  Python integers are taken as
  * int64 values or addresses (None is a null pointer), Python floats as float; each function
  * returns the entry point's result.  Optional: the Python package
  * falls back to ctypes when this module is absent.  Linked against libbiops.so in the same
@@ -11,6 +12,11 @@
 #include <string.h>
 
 #include "../../include/biops.h"
+
+/* HIP runtime (libamdhip64, a dependency of libbiops.so): the asynchronous copy the varlen
+ * wrapper uploads its work list with. */
+extern int hipMemcpyAsync(void* dst, const void* src, size_t bytes, int kind, void* stream);
+enum { kHipMemcpyHostToDevice = 1 };
 
 static int as_i64(PyObject* o, int64_t* v) {
   *v = (int64_t)PyLong_AsLongLong(o);
@@ -126,6 +132,19 @@ static PyObject* fast_sdpa_fused(PyObject* self, PyObject* const* args, Py_ssize
                                           fv[27], pv[28], pv[29]));
 }
 
+/* copy_h2d(dst, src, bytes, stream) -> hipError_t: hipMemcpyAsync host -> device on `stream` */
+static PyObject* fast_copy_h2d(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[4];
+  void* pv[4];
+  (void)self;
+  if (!parse(args, nargs, "pplp", iv, pv, NULL)) return NULL;
+  if (iv[2] < 0) {
+    PyErr_SetString(PyExc_ValueError, "negative copy size");
+    return NULL;
+  }
+  return PyLong_FromLong(hipMemcpyAsync(pv[0], pv[1], (size_t)iv[2], kHipMemcpyHostToDevice, pv[3]));
+}
+
 static PyMethodDef kMethods[] = {
     {"gemm", (PyCFunction)(void (*)(void))fast_gemm, METH_FASTCALL, "biops_gemm"},
     {"reduce", (PyCFunction)(void (*)(void))fast_reduce, METH_FASTCALL, "biops_reduce"},
@@ -136,6 +155,7 @@ static PyMethodDef kMethods[] = {
      "biops_varlen_fused_order"},
     {"varlen_sdpa_fused", (PyCFunction)(void (*)(void))fast_varlen_sdpa_fused, METH_FASTCALL,
      "biops_varlen_sdpa_fused"},
+    {"copy_h2d", (PyCFunction)(void (*)(void))fast_copy_h2d, METH_FASTCALL, "hipMemcpyAsync host to device"},
     {NULL, NULL, 0, NULL},
 };
 

@@ -142,6 +142,11 @@ def test_fast_call_module_matches_the_ctypes_binding():
         (nat.BF16, 0, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, 1.0, 256, null))] == [3, 0]
     with pytest.raises(TypeError):
         fast.sdpa_fused(*((nat.BF16, 1, 1, 1, 4, 4, 128, 128) + qkv + (null, 0, 0, 0, 0, 0, 0, "x", 256, null)))
+    # the work-list upload: argument errors raise before any HIP call
+    with pytest.raises(TypeError):
+        fast.copy_h2d(256, 256, 16)
+    with pytest.raises(ValueError):
+        fast.copy_h2d(256, 256, -1, null)
     if torch.cuda.is_available():
         assert nat.fast_function("biops_gemm") is fast.gemm
     else:  # the product path still insists on a GPU
