@@ -19,6 +19,7 @@ F32, F16, BF16, BOOL = 0, 1, 2, 3
 REDUCE_MEAN, REDUCE_L2 = 0, 1
 CAUSAL_NONE, CAUSAL_TOP_LEFT, CAUSAL_BOTTOM_RIGHT = 0, 1, 2
 
+ERR_ARG = 1  # BIOPS_ERR_ARG
 _STATUS = {
     1: "invalid argument",
     2: "unsupported layout",
@@ -70,6 +71,10 @@ _SIGNATURES = {
         [_i, _l, _l, _l, _l] + [_p, _l, _l] * 4 + [_p, _p, _p, _i, _f, _p],
     ),
     "biops_varlen_fused_order": (_l, [_p, _i, _p]),
+    "biops_varlen_sdpa_fused_planned": (
+        _i,
+        [_i, _l, _l, _l, _l] + [_p, _l, _l] * 4 + [_l, _l, _p, _p, _p, _l, _p, _i, _f, _p],
+    ),
     "biops_varlen_plan_len": (_l, [_l]),
     "biops_varlen_plan": (_l, [_l, _p, _p, _l, _l, _i, _p]),
     "biops_varlen_sdpa": (
@@ -176,7 +181,8 @@ def function(name: str):
 # same C functions and arguments, without ctypes' per-argument conversions.
 _FAST = {"biops_gemm": "gemm", "biops_reduce": "reduce", "biops_softmax": "softmax",
          "biops_sdpa_fused": "sdpa_fused", "biops_varlen_plan": "varlen_plan", "biops_varlen_fused_order": "varlen_fused_order",
-         "biops_varlen_sdpa_fused": "varlen_sdpa_fused"}
+         "biops_varlen_sdpa_fused": "varlen_sdpa_fused",
+         "biops_varlen_sdpa_fused_planned": "varlen_sdpa_fused_planned"}
 
 
 def fast_function(name: str):
@@ -205,9 +211,14 @@ def fast_copy_h2d():
     return _biops_fast.copy_h2d
 
 
+def last_error() -> str:
+    """The library's message for the calling thread's last failed call."""
+    return load(require_gpu=False).biops_last_error().decode(errors="replace")
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
-        msg = load(require_gpu=False).biops_last_error().decode(errors="replace")
+        msg = last_error()
         raise RuntimeError(f"{what} failed ({_STATUS.get(rc, rc)}): {msg}")
 
 

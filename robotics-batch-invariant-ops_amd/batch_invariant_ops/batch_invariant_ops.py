@@ -807,6 +807,25 @@ def varlen_scaled_dot_product_attention_batch_invariant(
         return output.zero_()
 
     nseq = cu_q.size - 1
+    if fused:
+        # one library call plans the work list and tile order into the pinned buffer, zeroes the
+        # rows no sequence writes, uploads the list and launches the fused kernel
+        with _VarlenStaging._lock:
+            st = _VarlenStaging.get(output.device, stream, _varlen_words(nseq, int(cu_q[-1]), True))
+            rc = _fast_fn("biops_varlen_sdpa_fused_planned")(
+                nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
+                q.data_ptr(), q.stride(1), q.stride(2),
+                k.data_ptr(), k.stride(1), k.stride(2),
+                v.data_ptr(), v.stride(1), v.stride(2),
+                output.data_ptr(), output.stride(1), output.stride(2), query.shape[1],
+                nseq, cu_q.ctypes.data, cu_kv.ctypes.data, st.host.data_ptr(), st.view.size,
+                st.dev.data_ptr(), causal, scale_value, stream,
+            )
+            st.event.record()
+        if rc == nat.ERR_ARG:
+            raise ValueError(nat.last_error())
+        nat.check(rc, "biops_varlen_sdpa_fused_planned")
+        return output
     with _VarlenStaging._lock:
         st = _VarlenStaging.get(output.device, stream, _varlen_words(nseq, int(cu_q[-1]), fused))
         # planner: validates the offsets (nondecreasing), drops empty sequences, and for the

@@ -748,3 +748,53 @@ extern "C" int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64
   a.pow2 = pow2_scale(scale);
   return launch_fused<0, true>(dtype, a, (hipStream_t)stream);
 }
+
+// Zeros of rows t < rows, heads h < hq of a [rows, hq, dv] output of 2-byte elements with byte
+// strides st_bytes, sh_bytes (unit stride inside a row); one thread per element.
+__global__ __launch_bounds__(256) void zero_rows_kernel(char* out, int64_t rows, int64_t hq, int64_t st_bytes,
+                                                        int64_t sh_bytes, int64_t row_bytes) {
+  const int64_t per = row_bytes / 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * hq * per) return;
+  const int64_t e = i % per, rh = i / per;
+  *reinterpret_cast<uint16_t*>(out + (rh / hq) * st_bytes + (rh % hq) * sh_bytes + 2 * e) = 0;
+}
+
+extern "C" int biops_varlen_sdpa_fused_planned(int dtype, int64_t hq, int64_t hkv, int64_t d, int64_t dv,
+                                               const void* q, int64_t sq_t, int64_t sq_h, const void* k,
+                                               int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t,
+                                               int64_t sv_h, void* out, int64_t so_t, int64_t so_h,
+                                               int64_t total_q, int64_t nseq, const int64_t* cu_q,
+                                               const int64_t* cu_kv, int64_t* host_buf, int64_t host_words,
+                                               int64_t* dev_buf, int causal, float scale, void* stream) {
+  if (!biops_varlen_fused_supported(dtype, d, dv))
+    return fail(BIOPS_ERR_DTYPE, "fused varlen attention takes bf16/fp16 with head dims <= 128, multiples of 8");
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(BIOPS_ERR_ARG, "invalid varlen head configuration");
+  if (total_q < 0 || nseq < 0 || !cu_q || !cu_kv || !host_buf || !dev_buf || !out)
+    return fail(BIOPS_ERR_ARG, "invalid varlen arguments");
+  if (cu_q[nseq] > total_q) return fail(BIOPS_ERR_ARG, "cumulative sequence lengths exceed packed tensor size");
+  const int64_t words = biops_varlen_plan_len(nseq);
+  if (words > host_words) return fail(BIOPS_ERR_SIZE, "work-list buffer of %lld words < %lld",
+                                      (long long)host_words, (long long)words);
+  if (biops_varlen_plan(nseq, cu_q, cu_kv, hq, dv, dtype, host_buf) < 0) return BIOPS_ERR_ARG;  // message set
+  hipStream_t s = (hipStream_t)stream;
+  // the kernel writes the rows of every sequence with keys; the rest (uncovered rows, sequences
+  // without keys) read zero
+  if (host_buf[3] != hq * total_q && total_q > 0 && dv > 0) {
+    const int64_t n = total_q * hq * dv;  // 2-byte elements
+    if (cdiv(n, 256) > 0x7fffffffLL) return fail(BIOPS_ERR_SIZE, "varlen output too large");
+    hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, (char*)out, total_q, hq,
+                       (int64_t)2 * so_t, (int64_t)2 * so_h, (int64_t)2 * dv);
+    const int rc = check_launch("zero_rows_kernel");
+    if (rc != BIOPS_OK) return rc;
+  }
+  if (host_buf[0] == 0) return BIOPS_OK;
+  if (words + host_buf[5] > host_words) return fail(BIOPS_ERR_SIZE, "work-list buffer of %lld words < %lld",
+                                                    (long long)host_words, (long long)(words + host_buf[5]));
+  const int64_t n = biops_varlen_fused_order(host_buf, causal, host_buf + words);
+  if (n < 0) return BIOPS_ERR_ARG;  // message set
+  if (hipMemcpyAsync(dev_buf, host_buf, sizeof(int64_t) * (size_t)(words + n), hipMemcpyHostToDevice, s) != hipSuccess)
+    return fail(BIOPS_ERR_HIP, "work-list upload failed");
+  return biops_varlen_sdpa_fused(dtype, hq, hkv, d, dv, q, sq_t, sq_h, k, sk_t, sk_h, v, sv_t, sv_h, out, so_t, so_h,
+                                 dev_buf, host_buf, dev_buf + words, causal, scale, stream);
+}

@@ -118,6 +118,21 @@ static PyObject* fast_varlen_sdpa_fused(PyObject* self, PyObject* const* args, P
                                                  (const int64_t*)pv[19], (int)iv[20], fv[21], pv[22]));
 }
 
+/* varlen_sdpa_fused_planned(dtype, hq, hkv, d, dv, q, sq_t, sq_h, k, sk_t, sk_h, v, sv_t, sv_h,
+ *                           out, so_t, so_h, total_q, nseq, cu_q, cu_kv, host_buf, host_words,
+ *                           dev_buf, causal, scale, stream) */
+static PyObject* fast_varlen_sdpa_fused_planned(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[27];
+  void* pv[27];
+  float fv[27];
+  (void)self;
+  if (!parse(args, nargs, "lllllpllpllpllpllllppplplfp", iv, pv, fv)) return NULL;
+  return PyLong_FromLong(biops_varlen_sdpa_fused_planned(
+      (int)iv[0], iv[1], iv[2], iv[3], iv[4], pv[5], iv[6], iv[7], pv[8], iv[9], iv[10], pv[11], iv[12], iv[13],
+      pv[14], iv[15], iv[16], iv[17], iv[18], (const int64_t*)pv[19], (const int64_t*)pv[20], (int64_t*)pv[21],
+      iv[22], (int64_t*)pv[23], (int)iv[24], fv[25], pv[26]));
+}
+
 /* sdpa_fused(dtype, batch, hq, hkv, lq, lk, d, dv, q, sqB, sqH, sqL, k, skB, skH, skL, v, svB,
  *            svH, svL, mask, mask_dtype, mB, mH, mI, mJ, causal, scale, out, stream) */
 static PyObject* fast_sdpa_fused(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
@@ -155,6 +170,8 @@ static PyMethodDef kMethods[] = {
      "biops_varlen_fused_order"},
     {"varlen_sdpa_fused", (PyCFunction)(void (*)(void))fast_varlen_sdpa_fused, METH_FASTCALL,
      "biops_varlen_sdpa_fused"},
+    {"varlen_sdpa_fused_planned", (PyCFunction)(void (*)(void))fast_varlen_sdpa_fused_planned, METH_FASTCALL,
+     "biops_varlen_sdpa_fused_planned"},
     {"copy_h2d", (PyCFunction)(void (*)(void))fast_copy_h2d, METH_FASTCALL, "hipMemcpyAsync host to device"},
     {NULL, NULL, 0, NULL},
 };
