@@ -700,29 +700,21 @@ class _VarlenStaging:
         self.event.record()
 
 
-def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, order_causal, out):
-    """The work list of biops_varlen_plan in ``out`` (int64 numpy array), followed, when
-    ``order_causal`` is a causal code, by the fused kernel's tile order
-    (biops_varlen_fused_order).  Returns (plan words, words used, workspace bytes)."""
+def _varlen_plan(cu_q, cu_kv, heads, value_dim, dtype, out):
+    """The work list of biops_varlen_plan in ``out`` (int64 numpy array).  Returns (plan words,
+    workspace bytes)."""
     nseq = len(cu_q) - 1
-    plan_fn = _fast_fn("biops_varlen_plan")
     words = int(nat.load().biops_varlen_plan_len(nseq))
-    ws_bytes = plan_fn(nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim, nat.dtype_code(dtype),
-                       out.ctypes.data)
+    ws_bytes = _fast_fn("biops_varlen_plan")(nseq, cu_q.ctypes.data, cu_kv.ctypes.data, heads, value_dim,
+                                             nat.dtype_code(dtype), out.ctypes.data)
     if ws_bytes < 0:
-        raise ValueError(nat.load().biops_last_error().decode())
-    used = words
-    if order_causal is not None and out[0] > 0:
-        n = _fast_fn("biops_varlen_fused_order")(out.ctypes.data, order_causal, out.ctypes.data + 8 * words)
-        if n < 0:
-            raise ValueError(nat.load().biops_last_error().decode())
-        used += int(n)
-    return words, used, ws_bytes
+        raise ValueError(nat.last_error())
+    return words, ws_bytes
 
 
 def _varlen_words(nseq, total_q, fused):
-    """Upper bound of the plan (and tile order) words: at most total_q / 128 + nseq query tiles
-    (each sequence adds at most one partial tile)."""
+    """Upper bound of the plan (and, for the fused kernel, tile order) words: at most
+    total_q / 128 + nseq query tiles (each sequence adds at most one partial tile)."""
     return 8 + 8 * nseq + (total_q // 128 + nseq if fused else 0)
 
 
@@ -826,32 +818,16 @@ def varlen_scaled_dot_product_attention_batch_invariant(
             raise ValueError(nat.last_error())
         nat.check(rc, "biops_varlen_sdpa_fused_planned")
         return output
+    # materialised path: plan (validates the offsets, drops empty sequences), zero the output
+    # (rows outside the sequences and of sequences without keys stay zero), upload, launch
     with _VarlenStaging._lock:
-        st = _VarlenStaging.get(output.device, stream, _varlen_words(nseq, int(cu_q[-1]), fused))
-        # planner: validates the offsets (nondecreasing), drops empty sequences, and for the
-        # fused kernel appends the tile order (longest key range first)
-        words, used, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype,
-                                             causal if fused else None, st.view)
+        st = _VarlenStaging.get(output.device, stream, _varlen_words(nseq, int(cu_q[-1]), False))
+        words, ws_bytes = _varlen_plan(cu_q, cu_kv, heads, value_dim, query.dtype, st.view)
         plan = st.view
         if plan[0] == 0:
             return output.zero_()
-        # The fused kernel writes every row of every sequence it computes (plan word 3 counts
-        # them per head); rows outside the sequences, or of a sequence with no keys, read zero.
-        if not (fused and int(plan[3]) == heads * query.shape[1]):
-            output.zero_()
-        dev = st.dev
-        st.upload(used, stream)
-        if fused:
-            rc = _fast_fn("biops_varlen_sdpa_fused")(
-                nat.dtype_code(query.dtype), heads, kv_heads, head_dim, value_dim,
-                q.data_ptr(), q.stride(1), q.stride(2),
-                k.data_ptr(), k.stride(1), k.stride(2),
-                v.data_ptr(), v.stride(1), v.stride(2),
-                output.data_ptr(), output.stride(1), output.stride(2),
-                dev.data_ptr(), plan.ctypes.data, dev.data_ptr() + 8 * words, causal, scale_value, stream,
-            )
-            nat.check(rc, "biops_varlen_sdpa_fused")
-            return output
+        output.zero_()
+        st.upload(words, stream)
         workspace = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=query.device)
         nat.call(
             "biops_varlen_sdpa",
@@ -860,7 +836,7 @@ def varlen_scaled_dot_product_attention_batch_invariant(
             k.data_ptr(), k.stride(1), k.stride(2),
             v.data_ptr(), v.stride(1), v.stride(2),
             output.data_ptr(), output.stride(1), output.stride(2),
-            dev.data_ptr(), plan.ctypes.data, causal, scale_value,
+            st.dev.data_ptr(), plan.ctypes.data, causal, scale_value,
             workspace.data_ptr(), workspace.numel(),
             stream,
         )
