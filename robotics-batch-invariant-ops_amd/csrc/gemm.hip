@@ -58,8 +58,8 @@ static const int kBigBN[kNumBig] = {256, 128, 256, 128, 64, 128, 64};
 // 64x128 block is rated above the 128x64 one: measured on MI355X it was 3-7 % faster on every
 // shape where both fill the same rounds (M=1024, N=2048, K=8192: 47.4 against 51.3 us; M=256,
 // N=8192, K=2048: 15.7 against 16.4 us).  The 64x64 block (rate unused) stays out of the
-// automatic choice: entry 6 (four 32x32 workgroups per unit) or entry 4 matched or beat it on
-// every shape measured (M=64..512 at N=8192, K=2048 and N=2048, K=8192).
+// cost model; it takes the long-K shapes of up to four 32x32 tiles per compute unit instead
+// of entry 6 (below).
 static const double kBigRate[kNumBig] = {1150, 1050, 1050, 850, 700, 720, 480};
 constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weighs
 // With a 16-bit N-major B (transposing LDS reads) each block is costed at this share of its
@@ -353,7 +353,11 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
       const double cost = (double)cdiv(tiles, cus) * kBigBM[i] * kBigBN[i] / rate;
       if (cost < best_cost) { best_cost = cost; best = kBigCfg + i; }
     }
-  if (best == 4 && prefer32) best = 6;
+  // There the four-wave 64x64 block (4-stage ring), where it applies, beat both (MI355X, all
+  // entries forced on one box: M = 512, N = 2048, K = 8192: 34.5 against 37.1 us for entry 6;
+  // M = 256: 33.3 against 34.5; M = 128, N = 8192, K = 2048: 11.6 against 12.4; M = 64: 10.9
+  // against 11.4).
+  if ((best == 4 || best == 6) && prefer32) best = (big_ok && !nmajor16) ? kBigCfg + 6 : 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
   return best;
 }

@@ -3,11 +3,11 @@
 // wavefront per SIMD, 16 independent 32x32 accumulators at 256 x 256, one at 64 x 64).  Blocks
 // from 256 x 256 down to 64 x 64; the ring takes as many stages as 160 KiB of LDS holds (2 at
 // 256 x 256, 10 at 64 x 64), except that K-major 128 x 128 blocks keep 3 and 128 x 64 / 64 x 128
-// blocks 4 (fewer in flight measured faster: same-box A/B in alternating order, 128 x 128 at
-// M = 2048, N = 2048, K = 8192 63.8 -> 62.4 us, 512 x 8192 x 2048 22.0 -> 21.2 us; 64 x 128 at
-// 256 x 8192 x 2048 16.0 -> 15.2 us, 1024 x 2048 x 8192 43.8 -> 43.3 us; 128 x 64 at
-// 512 x 8192 x 2048 28.2 -> 27.3 us; two stages are slower everywhere); one workgroup owns a
-// compute unit.
+// / 64 x 64 blocks 4 (fewer in flight measured faster: same-box A/B in alternating order,
+// 128 x 128 at M = 2048, N = 2048, K = 8192 63.8 -> 62.4 us, 512 x 8192 x 2048 22.0 -> 21.2 us;
+// 64 x 128 at 256 x 8192 x 2048 16.0 -> 15.2 us, 1024 x 2048 x 8192 43.8 -> 43.3 us; 128 x 64
+// at 512 x 8192 x 2048 28.2 -> 27.3 us; 64 x 64 at 128 x 8192 x 2048 12.1 -> 11.2 us; two stages
+// are slower everywhere).
 //
 // Same arithmetic as every other tile entry (gemm_core.h): 128-byte K steps in order, chunk
 // pairs q = 0..3 in order inside a step.  A stage of the LDS ring holds one K step (SB = 128
@@ -61,7 +61,10 @@ struct BigTile {
   static constexpr int LDS_STAGE = (BM + BN) * SB;
   static constexpr int LDS_MAX = 160 * 1024;
   static constexpr int MAX_STAGES = LDS_MAX / LDS_STAGE;
-  static constexpr int STAGES = !BKM ? MAX_STAGES : BM * BN == 128 * 128 ? 3 : BM * BN == 128 * 64 ? 4 : MAX_STAGES;
+  static constexpr int STAGES = !BKM ? MAX_STAGES
+                                : BM * BN == 128 * 128 ? 3
+                                : BM * BN == 128 * 64 || BM * BN == 64 * 64 ? 4
+                                : MAX_STAGES;
   static constexpr int RING = STAGES * LDS_STAGE;
   static constexpr int SMEM_BYTES = RING;
   static constexpr int A_LOADS = BM * CPR / THREADS;  // 16-byte chunks per thread per stage
