@@ -207,6 +207,23 @@ def test_fused_varlen_sequence_alone_equals_packed():
         assert_bitwise(alone, packed[:, s0:s1], f"sequence {s}")
 
 
+@pytest.mark.parametrize("causal_type", (None, "TopLeft"))
+def test_fused_varlen_sequence_without_keys_between_others(causal_type):
+    """A sequence with queries but no keys inside the pack reads zero (the reference skips it,
+    batch_invariant_ops.py:1296-1299); its neighbours match the oracle."""
+    ql, kl = (40, 7, 90), (30, 0, 90)
+    q = randn(1, sum(ql) + 3, 4, 32, seed=8360, dtype=torch.bfloat16)
+    k = randn(1, sum(kl), 2, 32, seed=8361, dtype=torch.bfloat16)
+    v = randn(1, sum(kl), 2, 32, seed=8362, dtype=torch.bfloat16)
+    cq, ck = _offsets(ql), _offsets(kl)
+    kw = dict(is_causal=causal_type is not None, causal_type=causal_type)
+    out = varlen(q.cuda(), k.cuda(), v.cuda(), cq.cuda(), ck.cuda(), **kw)
+    assert torch.count_nonzero(out[:, 40:47]) == 0
+    assert torch.count_nonzero(out[:, sum(ql):]) == 0
+    ref = oracle.varlen_sdpa(q, k, v, cq, ck, **kw)
+    check_attention(out, ref, v, torch.bfloat16)
+
+
 def test_fused_varlen_bottom_right_with_short_keys_zeroes_early_rows():
     """q_len > kv_len with bottom-right alignment: the first q_len - kv_len rows see no key."""
     ql, kl = (40,), (10,)
