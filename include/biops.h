@@ -215,12 +215,13 @@ int biops_varlen_sdpa_fused(int dtype, int64_t hq, int64_t hkv, int64_t d, int64
 
 /* biops_varlen_plan, biops_varlen_fused_order, the upload of both and biops_varlen_sdpa_fused in
  * one call, for callers holding the offsets on the host (the reference reads them there too,
- * batch_invariant_ops.py:1264-1265): cu_q / cu_kv are host arrays of nseq + 1 offsets, total_q
- * the packed query rows of q and out; host_buf (host_words int64, pinned host memory the caller
+ * batch_invariant_ops.py:1264-1265): cu_q / cu_kv are host arrays of nseq + 1 offsets (starting
+ * at zero, nondecreasing, within total_q query rows of q and out and total_kv key rows of k and
+ * v, as the reference requires; BIOPS_ERR_ARG otherwise); host_buf (host_words int64, pinned host memory the caller
  * leaves untouched until the upload has run on `stream`) receives the plan followed by the tile
  * order, and dev_buf (device, as many words) their copy.  Rows of out outside every sequence,
  * and rows of sequences without keys, are zeroed first.  Returns BIOPS_ERR_ARG (message in
- * biops_last_error) for offsets the planner rejects, BIOPS_ERR_SIZE when host_words is below
+ * biops_last_error) for rejected offsets, BIOPS_ERR_SIZE when host_words is below
  * biops_varlen_plan_len(nseq) plus the plan's query-tile count; otherwise as
  * biops_varlen_sdpa_fused.  Replaces varlen_scaled_dot_product_attention_batch_invariant
  * (batch_invariant_ops.py:1216-1344) from its offsets on. */
@@ -229,7 +230,7 @@ int biops_varlen_sdpa_fused_planned(int dtype, int64_t hq, int64_t hkv, int64_t 
                                     const void* k, int64_t sk_t, int64_t sk_h,
                                     const void* v, int64_t sv_t, int64_t sv_h,
                                     void* out, int64_t so_t, int64_t so_h, int64_t total_q,
-                                    int64_t nseq, const int64_t* cu_q, const int64_t* cu_kv,
+                                    int64_t total_kv, int64_t nseq, const int64_t* cu_q, const int64_t* cu_kv,
                                     int64_t* host_buf, int64_t host_words, int64_t* dev_buf,
                                     int causal, float scale, void* stream);
 

@@ -73,7 +73,7 @@ _SIGNATURES = {
     "biops_varlen_fused_order": (_l, [_p, _i, _p]),
     "biops_varlen_sdpa_fused_planned": (
         _i,
-        [_i, _l, _l, _l, _l] + [_p, _l, _l] * 4 + [_l, _l, _p, _p, _p, _l, _p, _i, _f, _p],
+        [_i, _l, _l, _l, _l] + [_p, _l, _l] * 4 + [_l, _l, _l, _p, _p, _p, _l, _p, _i, _f, _p],
     ),
     "biops_varlen_plan_len": (_l, [_l]),
     "biops_varlen_plan": (_l, [_l, _p, _p, _l, _l, _i, _p]),

@@ -809,7 +809,7 @@ def varlen_scaled_dot_product_attention_batch_invariant(
                 q.data_ptr(), q.stride(1), q.stride(2),
                 k.data_ptr(), k.stride(1), k.stride(2),
                 v.data_ptr(), v.stride(1), v.stride(2),
-                output.data_ptr(), output.stride(1), output.stride(2), query.shape[1],
+                output.data_ptr(), output.stride(1), output.stride(2), query.shape[1], key.shape[1],
                 nseq, cu_q.ctypes.data, cu_kv.ctypes.data, st.host.data_ptr(), st.view.size,
                 st.dev.data_ptr(), causal, scale_value, stream,
             )

@@ -764,15 +764,18 @@ extern "C" int biops_varlen_sdpa_fused_planned(int dtype, int64_t hq, int64_t hk
                                                const void* q, int64_t sq_t, int64_t sq_h, const void* k,
                                                int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t,
                                                int64_t sv_h, void* out, int64_t so_t, int64_t so_h,
-                                               int64_t total_q, int64_t nseq, const int64_t* cu_q,
+                                               int64_t total_q, int64_t total_kv, int64_t nseq, const int64_t* cu_q,
                                                const int64_t* cu_kv, int64_t* host_buf, int64_t host_words,
                                                int64_t* dev_buf, int causal, float scale, void* stream) {
   if (!biops_varlen_fused_supported(dtype, d, dv))
     return fail(BIOPS_ERR_DTYPE, "fused varlen attention takes bf16/fp16 with head dims <= 128, multiples of 8");
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(BIOPS_ERR_ARG, "invalid varlen head configuration");
-  if (total_q < 0 || nseq < 0 || !cu_q || !cu_kv || !host_buf || !dev_buf || !out)
+  if (total_q < 0 || total_kv < 0 || nseq < 0 || !cu_q || !cu_kv || !host_buf || !dev_buf || !out)
     return fail(BIOPS_ERR_ARG, "invalid varlen arguments");
-  if (cu_q[nseq] > total_q) return fail(BIOPS_ERR_ARG, "cumulative sequence lengths exceed packed tensor size");
+  // the offsets' own rules (batch_invariant_ops.py:1264-1269); the planner rejects decreasing ones
+  if (cu_q[0] != 0 || cu_kv[0] != 0) return fail(BIOPS_ERR_ARG, "cumulative sequence lengths must start at zero");
+  if (cu_q[nseq] > total_q || cu_kv[nseq] > total_kv)
+    return fail(BIOPS_ERR_ARG, "cumulative sequence lengths exceed packed tensor size");
   const int64_t words = biops_varlen_plan_len(nseq);
   if (words > host_words) return fail(BIOPS_ERR_SIZE, "work-list buffer of %lld words < %lld",
                                       (long long)host_words, (long long)words);

@@ -119,18 +119,18 @@ static PyObject* fast_varlen_sdpa_fused(PyObject* self, PyObject* const* args, P
 }
 
 /* varlen_sdpa_fused_planned(dtype, hq, hkv, d, dv, q, sq_t, sq_h, k, sk_t, sk_h, v, sv_t, sv_h,
- *                           out, so_t, so_h, total_q, nseq, cu_q, cu_kv, host_buf, host_words,
- *                           dev_buf, causal, scale, stream) */
+ *                           out, so_t, so_h, total_q, total_kv, nseq, cu_q, cu_kv, host_buf,
+ *                           host_words, dev_buf, causal, scale, stream) */
 static PyObject* fast_varlen_sdpa_fused_planned(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
-  int64_t iv[27];
-  void* pv[27];
-  float fv[27];
+  int64_t iv[28];
+  void* pv[28];
+  float fv[28];
   (void)self;
-  if (!parse(args, nargs, "lllllpllpllpllpllllppplplfp", iv, pv, fv)) return NULL;
+  if (!parse(args, nargs, "lllllpllpllpllplllllppplplfp", iv, pv, fv)) return NULL;
   return PyLong_FromLong(biops_varlen_sdpa_fused_planned(
       (int)iv[0], iv[1], iv[2], iv[3], iv[4], pv[5], iv[6], iv[7], pv[8], iv[9], iv[10], pv[11], iv[12], iv[13],
-      pv[14], iv[15], iv[16], iv[17], iv[18], (const int64_t*)pv[19], (const int64_t*)pv[20], (int64_t*)pv[21],
-      iv[22], (int64_t*)pv[23], (int)iv[24], fv[25], pv[26]));
+      pv[14], iv[15], iv[16], iv[17], iv[18], iv[19], (const int64_t*)pv[20], (const int64_t*)pv[21],
+      (int64_t*)pv[22], iv[23], (int64_t*)pv[24], (int)iv[25], fv[26], pv[27]));
 }
 
 /* sdpa_fused(dtype, batch, hq, hkv, lq, lk, d, dv, q, sqB, sqH, sqL, k, skB, skH, skL, v, svB,

@@ -147,11 +147,15 @@ def test_fast_call_module_matches_the_ctypes_binding():
     cu_dec = np.array([0, 5, 3], dtype=np.int64)
     cu_ok = np.array([0, 5, 9], dtype=np.int64)
     hb = np.zeros(64, dtype=np.int64)
-    def planned(dtype, cuq, cuk, words, total=9):
-        return (dtype, 8, 2, 64, 64) + (256, 8 * 64, 64) * 4 + (total, 2, cuq.ctypes.data, cuk.ctypes.data,
-                                                                  hb.ctypes.data, words, 256, 2, 0.125, null)
+    cu_one = np.array([1, 5, 9], dtype=np.int64)
+
+    def planned(dtype, cuq, cuk, words, total=9, total_kv=9):
+        return (dtype, 8, 2, 64, 64) + (256, 8 * 64, 64) * 4 + (total, total_kv, 2, cuq.ctypes.data,
+                                                                  cuk.ctypes.data, hb.ctypes.data, words, 256, 2,
+                                                                  0.125, null)
     for args, rc in ((planned(nat.BF16, cu_dec, cu_ok, 64), 1), (planned(nat.BF16, cu_ok, cu_ok, 8), 5),
-                     (planned(nat.F32, cu_ok, cu_ok, 64), 3), (planned(nat.BF16, cu_ok, cu_ok, 64, total=8), 1)):
+                     (planned(nat.F32, cu_ok, cu_ok, 64), 3), (planned(nat.BF16, cu_ok, cu_ok, 64, total=8), 1),
+                     (planned(nat.BF16, cu_ok, cu_ok, 64, total_kv=8), 1), (planned(nat.BF16, cu_one, cu_ok, 64), 1)):
         assert fast.varlen_sdpa_fused_planned(*args) == L.biops_varlen_sdpa_fused_planned(*args) == rc
     assert fast.varlen_sdpa_fused_planned(*planned(nat.BF16, cu_dec, cu_ok, 64)) == 1
     assert "nondecreasing" in nat.last_error()
