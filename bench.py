@@ -71,8 +71,9 @@ def profile_kernel(which, iters):
         v = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).cuda()
         for _ in range(iters):
             bio.scaled_dot_product_attention_batch_invariant(q, k, v, is_causal=True, enable_gqa=True)
-    elif which == "moe":
-        # configs[4] at T = 4096, selected routes (the default evaluation)
+    elif which in ("moe", "moe_t1"):
+        # configs[4] at T = 4096 (moe) or its first token alone (moe_t1, the one-token split of
+        # the config), selected routes (the default evaluation)
         from batch_invariant_ops.moe import _moe
 
         g = torch.Generator().manual_seed(5)
@@ -82,8 +83,9 @@ def profile_kernel(which, iters):
         probs = torch.softmax(torch.randn(4096, 64, generator=g), -1)
         wts, sel = torch.topk(probs, 8, dim=-1)
         wts, sel = wts.cuda(), sel.cuda()
+        t = 1 if which == "moe_t1" else 4096
         for _ in range(iters):
-            _moe(hidden, wts, sel, gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2),
+            _moe(hidden[:t], wts[:t], sel[:t], gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2),
                  dn.transpose(1, 2), sparse=True)
     elif which == "varlen":
         # 32 packed sequences, bottom-right causal (fused varlen kernel)
@@ -141,11 +143,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "gemm_mid", "copy", "sdpa", "varlen", "moe", "softmax", "norm"),
+        choices=("gemm", "gemm_mid", "copy", "sdpa", "varlen", "moe", "moe_t1", "softmax", "norm"),
         default=None,
         help="only launch the roofline kernel (gemm), the M=1024 8192->2048 linear (gemm_mid), a "
         "512 MiB device copy (copy), configs[2] causal attention at B=16 (sdpa), configs[3] varlen "
-        "attention (varlen), configs[4] MoE at T=4096 (moe), a 262144x1024 bf16 softmax (softmax) or "
+        "attention (varlen), configs[4] MoE at T=4096 (moe) or T=1 (moe_t1), a 262144x1024 bf16 softmax (softmax) or "
         "a 65536x2048 bf16 row L2 norm (norm) --iters times, for counter runs; prints no JSON line",
     )
     p.add_argument("--iters", type=int, default=10)

@@ -108,7 +108,10 @@ int biops_gemm_tile_count(void);
  * choice for fp32; entries 12 (one 32x32 block per workgroup with loader wavefronts, for few
  * rows) and 13-19 (blocks of 256x256, 256x128, 128x256, 128x128, 128x64, 64x128 and 64x64 on
  * four wavefronts, 16-bit types only) need K-major B, 16-byte aligned rows and K a multiple of
- * 128 bytes and fall back to the automatic choice elsewhere.
+ * 128 bytes and fall back to the automatic choice elsewhere.  Entries 20 and 21 (the
+ * weight-streaming tile: 16- or 32-row m-tiles x 64 output columns, for grouped rows with few
+ * rows per group) serve only the MoE expert GEMMs with 16-bit N-major weights, 16-byte aligned
+ * rows and K a multiple of 128 bytes, and fall back to the automatic choice elsewhere.
  * For tuning and for the cross-entry bitwise tests.  No reference counterpart. */
 int biops_set_gemm_tile(int cfg);
 
@@ -292,7 +295,8 @@ int64_t biops_moe_workspace_size(int dtype, int64_t tokens, int64_t experts, int
  *                 round(w[t,s])) and each partial sum rounded to dtype
  * x[T,D] (row stride sx), gate/up given as [E,I,D] views with strides (sgE, sgI, sgD) and
  * (suE, suI, suD), down as [E,D,I] with (sdE, sdD, sdI); each needs its D (resp. I) stride or
- * its I (resp. D) stride equal to 1.  weights[T,k] fp32/dtype (w_dtype), sel[T,k] int64.
+ * its I (resp. D) stride equal to 1.  weights[T,k] in any float dtype w_dtype (each weight is
+ * rounded to dtype before the multiply, round(w[t,s]) above), sel[T,k] int64.
  * Expert indices outside [0,E) make the call write zeros for that token and set *bad_index
  * (device int32, may be NULL) to 1.  out[T,D] contiguous.
  * Replaces deterministic_token_choice_moe (moe.py:11-92). */

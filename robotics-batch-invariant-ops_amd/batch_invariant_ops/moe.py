@@ -89,8 +89,13 @@ def _moe(
     if gate.stride() != up.stride():
         gate, up = gate.contiguous(), up.contiguous()
     down = _unit_stride_weight(down_weight)
-    # routing_weights.to(activation dtype), as the reference does before the multiply
-    weights = routing_weights.to(dtype).contiguous()
+    # The kernels round each routing weight to the activation dtype before the multiply (the
+    # reference's routing_weights.to(dtype), moe.py:87), so float weights go in as they are.
+    w_code = nat.DIRECT_DTYPES.get(routing_weights.dtype)
+    if w_code is None:
+        weights, w_code = routing_weights.to(dtype).contiguous(), code
+    else:
+        weights = routing_weights.contiguous()
     selected = selected_experts.to(torch.int64).contiguous()
 
     out = torch.empty((token_count, hidden_size), dtype=dtype, device=x.device)
@@ -113,7 +118,7 @@ def _moe(
         gate.data_ptr(), *gate.stride(),
         up.data_ptr(), *up.stride(),
         down.data_ptr(), *down.stride(),
-        weights.data_ptr(), code, selected.data_ptr(),
+        weights.data_ptr(), w_code, selected.data_ptr(),
         out.data_ptr(), bad.data_ptr() if check else None,
         scratch.data_ptr(), scratch.numel(),
         nat.stream_of(out),

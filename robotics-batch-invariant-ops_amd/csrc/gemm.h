@@ -43,6 +43,8 @@ struct BmmArgs {
 
 constexpr int kGrpHeader = 4;
 constexpr int kGrpStride = 4;
+// Smallest m-tile height grouped_tile_rows() returns (tables of grouped launches are sized for it).
+constexpr int kMinGroupedTileRows = 16;
 
 int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream);
 

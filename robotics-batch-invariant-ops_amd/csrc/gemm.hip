@@ -7,6 +7,7 @@
 #include "gemm.h"
 #include "gemm_big.h"
 #include "gemm_skinny.h"
+#include "gemm_stream.h"
 
 namespace biops {
 
@@ -68,7 +69,15 @@ constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weigh
 // 2048 x 6144 x 4096, 1024 x 4096 x 4096, 512 x 8192 x 2048; the 256x256 block 0.86-0.96,
 // 0.96 on the shapes it wins).
 static const double kBigNmajorShare[kNumBig] = {0.93, 0.91, 0.87, 0.87, 0.88, 0.79, 0.86};
-constexpr int kMenuSize = kBigCfg + kNumBig;
+constexpr int kBigEnd = kBigCfg + kNumBig;
+// Entries 20 and 21: the weight-streaming tile (gemm_stream.h), one m-tile of 16 (entry 20) or 32
+// (entry 21) rows x 64 output columns per workgroup.  Grouped rows with a 16-bit N-major B
+// only (the MoE expert GEMMs); elsewhere they fall back to the automatic choice.
+constexpr int kStreamCfg = kBigEnd;
+constexpr int kNumStream = 2;
+static const int kStreamBM[kNumStream] = {16, 32};
+static_assert(kMinGroupedTileRows == 16, "grouped tables are sized for the 16-row stream entry");
+constexpr int kMenuSize = kStreamCfg + kNumStream;
 
 // One persistent workgroup walks tiles t = slot, slot + G, ... over all batch elements.
 // Epilogues: plain C = round(acc (+ bias[n])) (bias added in fp32 before the single rounding);
@@ -312,7 +321,10 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // or the same with a 16-bit N-major B; 32-bit output offsets inside a 256-row tile.
   const bool big_ok = (skinny_ok || (nmajor16 && !swiglu && !grouped)) && dtype != BIOPS_F32 &&
                       a.ldc < (int64_t(1) << 23);
-  if (forced >= kBigCfg && forced < kMenuSize && big_ok) return forced;
+  if (forced >= kBigCfg && forced < kBigEnd && big_ok) return forced;
+  // The weight-streaming entries: grouped rows, 16-bit N-major B on the direct path.
+  const bool stream_ok = grouped && nmajor16;
+  if (forced >= kStreamCfg && forced < kMenuSize && stream_ok) return forced;
   if (cfg_ok(dtype, forced, swiglu, grouped)) return forced;
   const int cus = device_cus();
   const int64_t batch = a.nb1 * a.nb2;
@@ -359,6 +371,13 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // against 11.4).
   if ((best == 4 || best == 6) && prefer32) best = (big_ok && !nmajor16) ? kBigCfg + 6 : 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
+  // Grouped rows of at most 16 rows per group on average with a 16-bit N-major B (the MoE
+  // expert GEMMs of calls up to about 2E/k tokens): the weight-streaming entries.  MI355X, C5
+  // shapes (E = 64, D = 2048, I = 768, top-8), per sparse MoE call against the best table entry:
+  // 1 token 47.1 us (16 rows) against 62.8 (entry 7); 2 tokens 56.3 against 74.5 (entry 2);
+  // 32 tokens 154.6 (32 rows) against 171.4; 128 tokens 163.5 (32 rows) against 177.7; at 256
+  // tokens (32 rows per group) entry 2 wins, 180.1 against 207.2.
+  if (stream_ok && mean <= 16) best = mean <= 2 ? kStreamCfg : kStreamCfg + 1;
   return best;
 }
 
@@ -385,6 +404,53 @@ static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
   if (row_blocks * cdiv(a.N, 8) <= cus) return launch_skinny_block<T, AR, 8>(a, stream);
   if (row_blocks * cdiv(a.N, 16) <= cus) return launch_skinny_block<T, AR, 16>(a, stream);
   return launch_skinny_block<T, AR, 32>(a, stream);
+}
+
+// Grouped rows, 16-bit N-major B: one m-tile x 64 output columns per workgroup.  Like the
+// one-tile-per-workgroup grouped entries, XCD x (workgroups g with g % 8 == x) takes the x-th
+// eighth of the tiles; the tiles are numbered column-block-major, so the m-tiles of one group
+// and column block (the same weights) fall on one XCD and its L2.
+template <typename T, int BM, bool SWIGLU>
+__global__ __launch_bounds__(256) void stream_kernel(BmmArgs args) {
+  using S = StreamTile<T, BM, SWIGLU>;
+  __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
+  const uint32_t J = (uint32_t)args.grp[0];
+  const uint32_t total = J * (uint32_t)args.tiles_n;
+  const uint32_t per = (total + 7u) / 8u;
+  const uint32_t i = blockIdx.x / 8u, x = blockIdx.x % 8u;
+  const uint32_t t = x * per + i;
+  if (i >= per || t >= total) return;
+  const uint32_t tn = t / J, tm = t - tn * J;
+  const int32_t* e = args.grp + kGrpHeader + kGrpStride * tm;
+  const int64_t m0 = e[1], rows = e[2] - e[1];
+  const int64_t n0 = (int64_t)tn * S::OUT;
+  const int64_t boff = (int64_t)e[0] * args.sB1 + n0;
+  typename S::Sources src;
+  src.A = reinterpret_cast<const T*>(args.A);
+  src.lda = args.lda;
+  src.a_rows = args.a_rows;
+  src.m0 = m0;
+  src.rows = rows < BM ? (int)rows : BM;
+  src.bg = reinterpret_cast<const T*>(args.B) + boff;
+  src.bu = reinterpret_cast<const T*>(SWIGLU ? args.B2 : args.B) + boff;
+  src.ldb = args.ldb;
+  src.ncols = args.N - n0;
+  src.K = args.K;
+  const typename S::Acc acc = S::run(smem, src);
+  S::store(acc, reinterpret_cast<T*>(args.C) + m0 * args.ldc + n0, args.ldc, src.rows, src.ncols);
+}
+
+template <typename T, int BM, bool SWIGLU>
+static int launch_stream(const BmmArgs& a0, hipStream_t stream) {
+  BmmArgs a = a0;
+  a.tiles_m = cdiv(a.grp_rows, BM) + std::min(a.grp_groups, a.grp_rows);
+  a.tiles_n = cdiv(a.N, StreamTile<T, BM, SWIGLU>::OUT);
+  a.total = a.tiles_m * a.tiles_n;
+  if (a.total == 0) return BIOPS_OK;
+  if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  const int64_t grid = (a.total + 7) & ~int64_t(7);
+  hipLaunchKernelGGL((stream_kernel<T, BM, SWIGLU>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  return check_launch("stream_kernel");
 }
 
 template <typename T, int BM, int BN, int SB, bool BKM>
@@ -449,6 +515,12 @@ static int launch_grouped_typed(const BmmArgs& a, bool b_kmajor, bool direct, in
     case 6: if constexpr (kPlain) return launch_layout<T, 6, EPI, true>(a, b_kmajor, direct, s); break;
     case 7: if constexpr (!kPlain) return launch_layout<T, 7, EPI, true>(a, b_kmajor, direct, s); break;
     case 11: if constexpr (kPlain) return launch_layout<T, 11, EPI, true>(a, b_kmajor, direct, s); break;
+    case kStreamCfg:
+      if constexpr (sizeof(T) == 2) return launch_stream<T, 16, !kPlain>(a, s);
+      break;
+    case kStreamCfg + 1:
+      if constexpr (sizeof(T) == 2) return launch_stream<T, 32, !kPlain>(a, s);
+      break;
     default: break;
   }
   return fail(BIOPS_ERR_ARG, "no grouped kernel for tile config %d", cfg);
@@ -548,6 +620,7 @@ int grouped_tile_rows(int dtype, BmmArgs a, int epi, bool b_kmajor) {
   if (dtype_bytes(dtype) == 0) return 0;
   bool direct;
   const int cfg = prepare_bmm(dtype, a, epi, b_kmajor, direct);
+  if (cfg >= kStreamCfg && cfg < kMenuSize) return kStreamBM[cfg - kStreamCfg];
   return cfg >= 0 && cfg < kNumCfg ? kCfgBM[cfg] : 0;
 }
 

@@ -98,6 +98,16 @@ struct BSource {
   }
 };
 
+// SwiGLU output of one element from its gate and up accumulators, before the rounding of the
+// store: round(silu(round(g))) * round(u) (the product of two rounded 16-bit values is exact in
+// fp32).  Every kernel with the SwiGLU epilogue calls this one function.
+template <typename T>
+__device__ __forceinline__ float swiglu_value(float g_acc, float u_acc) {
+  const float g = Num<T>::round(g_acc);
+  const float u = Num<T>::round(u_acc);
+  return Num<T>::round(g / (1.0f + expf(-g))) * u;
+}
+
 // LDS tile layout: rows of 128 bytes (one K step), unpadded; 16-byte chunk c of row r lives in
 // slot c ^ ((r >> 1) & 7).  Sixteen consecutive rows reading the same chunk hit 16 distinct
 // (half-row, slot) bank groups, so the MFMA operand reads (ds_read_b128) are conflict-free.
@@ -625,9 +635,7 @@ struct GemmTile {
         for (int r = 0; r < 16; ++r) {
           float v;
           if constexpr (SWIGLU) {
-            const float g = Num<T>::round(acc[i][j][r]);
-            const float u = Num<T>::round(acc[i][j + 1][r]);
-            v = Num<T>::round(g / (1.0f + expf(-g))) * u;
+            v = swiglu_value<T>(acc[i][j][r], acc[i][j + 1][r]);
           } else {
             v = bias ? acc[i][j][r] + bv : acc[i][j][r];
           }

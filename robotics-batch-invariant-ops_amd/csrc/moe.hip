@@ -294,7 +294,6 @@ __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
   }
 }
 
-// One wavefront per route: its packed row, and its token's row of x copied there.
 // Packed row of every route (route_row[r], -1 for an invalid expert index) and the token of
 // every packed row (row_token[row] = r / k): the gate/up GEMM reads its A rows through that
 // table, so no copy of x is made.  One thread per route.
@@ -309,6 +308,109 @@ __global__ __launch_bounds__(256) void moe_route_rows_kernel(PackArgs a) {
   if (ok) a.row_token[row] = (int32_t)(r / a.k);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Route packing of a small call in one workgroup: the rank, plan and route-row kernels above
+// in one launch, with the same route rows, token table, expert offsets and m-tile tables
+// (a few-token call otherwise spends three kernel latencies on eight routes).  Thread r owns
+// route r; the lanes of one wavefront holding the same bucket find each other by ballots, and
+// bucket b's count per wavefront goes to LDS; thread b then turns the 16 counts into the routes
+// of earlier wavefronts, and a workgroup scan over the buckets places rows and m-tiles.
+constexpr int kSmallPackRoutes = 1024;  // routes (one per thread)
+constexpr int kSmallPackBuckets = 512;  // experts + 1 (the bucket of invalid indices)
+constexpr int kSmallPackWaves = kSmallPackRoutes / 64;
+
+__global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackArgs a) {
+  __shared__ int32_t cnt[kSmallPackWaves][kSmallPackBuckets];
+  __shared__ int32_t first_row[kSmallPackBuckets];
+  __shared__ int32_t wsum[kSmallPackWaves][3];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int E = (int)a.E, E1 = E + 1;
+  for (int b = lane; b < E1; b += 64) cnt[w][b] = 0;
+  const bool valid = tid < a.R;
+  int bucket = E;
+  if (valid) {
+    const int64_t e = a.sel[tid];
+    if (e >= 0 && e < a.E) bucket = (int)e;
+  }
+  const int nbits = 32 - __clz(E);
+  uint64_t same = __ballot(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = (bucket >> bit) & 1;
+    const uint64_t m = __ballot(valid && on);
+    same &= on ? m : ~m;
+  }
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int lower = __popcll(same & below);
+  // each wavefront writes only its own row of cnt (zeroed above by the same wavefront)
+  if (valid && lower == 0) cnt[w][bucket] = __popcll(same);
+  __syncthreads();
+  int32_t n = 0;  // routes of bucket tid
+  if (tid < E1) {
+    for (int v = 0; v < kSmallPackWaves; ++v) {
+      const int32_t c = cnt[v][tid];
+      cnt[v][tid] = n;
+      n += c;
+    }
+  }
+  const bool expert = tid < E;
+  const int32_t rows = expert ? n : 0;
+  const int32_t t1 = expert ? (n + a.bm1 - 1) / a.bm1 : 0;
+  const int32_t t2 = expert ? (n + a.bm2 - 1) / a.bm2 : 0;
+  const int32_t ir = wave_incl_scan(rows), i1 = wave_incl_scan(t1), i2 = wave_incl_scan(t2);
+  if (lane == 63) {
+    wsum[w][0] = ir;
+    wsum[w][1] = i1;
+    wsum[w][2] = i2;
+  }
+  __syncthreads();
+  int32_t pr = 0, p1 = 0, p2 = 0;
+  for (int v = 0; v < w; ++v) {
+    pr += wsum[v][0];
+    p1 += wsum[v][1];
+    p2 += wsum[v][2];
+  }
+  const int32_t row0 = pr + ir - rows;
+  if (tid < E1) {
+    first_row[tid] = row0;
+    a.off[tid] = row0;
+  }
+  if (expert) {
+    int32_t j = p1 + i1 - t1;
+    for (int32_t m = 0; m < n; m += a.bm1, ++j) {
+      int32_t* g = a.grp1 + kGrpHeader + kGrpStride * j;
+      g[0] = tid; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
+    }
+    j = p2 + i2 - t2;
+    for (int32_t m = 0; m < n; m += a.bm2, ++j) {
+      int32_t* g = a.grp2 + kGrpHeader + kGrpStride * j;
+      g[0] = tid; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
+    }
+  }
+  if (tid == kSmallPackRoutes - 1) {
+    a.grp1[0] = p1 + i1;
+    a.grp2[0] = p2 + i2;
+  }
+  __syncthreads();
+  if (valid) {
+    int32_t row = -1;
+    if (bucket < E) {
+      row = first_row[bucket] + cnt[w][bucket] + lower;
+      a.row_token[row] = (int32_t)(tid / a.k);
+    }
+    a.route_row[tid] = row;
+  }
+}
+
 // Workspace of the sparse path (byte offsets, 256-byte aligned).
 struct SparseLayout {
   int64_t y, act, rank, route, token, counts, off, grp1, grp2, total;
@@ -317,8 +419,8 @@ struct SparseLayout {
 static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int64_t I) {
   auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
   const int64_t S = cdiv(R, route_chunk(R));
-  // Tile tables sized for the smallest tile height of the menu (32 rows).
-  const int64_t tiles = cdiv(R, 32) + std::min(E, R);
+  // Tile tables sized for the smallest m-tile height of the grouped entries.
+  const int64_t tiles = cdiv(R, kMinGroupedTileRows) + std::min(E, R);
   SparseLayout L;
   int64_t p = 0;
   L.y = p; p += al(R * D * elt);  // packed down-projection rows
@@ -498,7 +600,7 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
     }
     const int bm1 = grouped_tile_rows(dtype, g.gu, kEpiSwiglu, g.gu_kmajor);
     const int bm2 = grouped_tile_rows(dtype, g.dn, kEpiPlain, g.dn_kmajor);
-    if (bm1 < 32 || bm2 < 32) return fail(BIOPS_ERR_ARG, "no grouped GEMM tile");
+    if (bm1 < kMinGroupedTileRows || bm2 < kMinGroupedTileRows) return fail(BIOPS_ERR_ARG, "no grouped GEMM tile");
 
     PackArgs p{};
     p.sel = sel;
@@ -513,13 +615,18 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
     p.chunk = route_chunk(R);
     p.S = cdiv(R, p.chunk);
     p.bm1 = bm1; p.bm2 = bm2;
-    const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
-    hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)cdiv(p.S, kRankWaves)), dim3(256), hist_bytes, s, p);
-    if ((rc = check_launch("moe_rank_kernel")) != BIOPS_OK) return rc;
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    if ((rc = check_launch("moe_plan_kernel")) != BIOPS_OK) return rc;
-    hipLaunchKernelGGL(moe_route_rows_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, s, p);
-    if ((rc = check_launch("moe_route_rows_kernel")) != BIOPS_OK) return rc;
+    if (R <= kSmallPackRoutes && experts + 1 <= kSmallPackBuckets) {
+      hipLaunchKernelGGL(moe_pack_small_kernel, dim3(1), dim3(kSmallPackRoutes), 0, s, p);
+      if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
+    } else {
+      const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
+      hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)cdiv(p.S, kRankWaves)), dim3(256), hist_bytes, s, p);
+      if ((rc = check_launch("moe_rank_kernel")) != BIOPS_OK) return rc;
+      hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
+      if ((rc = check_launch("moe_plan_kernel")) != BIOPS_OK) return rc;
+      hipLaunchKernelGGL(moe_route_rows_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, s, p);
+      if ((rc = check_launch("moe_route_rows_kernel")) != BIOPS_OK) return rc;
+    }
     if ((rc = launch_bmm(dtype, g.gu, kEpiSwiglu, g.gu_kmajor, s)) != BIOPS_OK) return rc;
     if ((rc = launch_bmm(dtype, g.dn, kEpiPlain, g.dn_kmajor, s)) != BIOPS_OK) return rc;
   }

@@ -5,8 +5,9 @@ rows of its launch are, so evaluating only the selected routes must reproduce th
 bits exactly; the dense path itself is pinned to the oracle in test_gpu_moe.py.  The cases cover
 the packing's corners: several route chunks (over 1024 routes), every route on one expert,
 duplicate experts inside a token, empty experts, E = 1 and E not a power of two, out-of-range
-indices, hidden sizes that are not a multiple of 8 (no 16-byte rows), N-major weights, and every
-tile entry of the grouped GEMM.
+indices, hidden sizes that are not a multiple of 8 (no 16-byte rows), N-major weights, every
+tile entry of the grouped GEMM (the weight-streaming entries of few-token calls among them),
+and both sides of the limits of the one-workgroup packing.
 """
 
 import pytest
@@ -170,3 +171,62 @@ def test_sparse_c5_shape_batch_invariant():
     assert_bitwise(one, sparse[:1], "token 0 alone")
     mid = _moe(hidden[100:356], w[100:356], sel[100:356], gate, up, down, sparse=True)
     assert_bitwise(mid, sparse[100:356], "tokens 100..355")
+
+
+def nmajor_weights(E, I, D, seed, dtype, scale=0.1):
+    """Fused [E, D, 2I] gate/up and [E, I, D] down storage (the reference MoE's layout): the
+    gate / up / down views are N-major, the layout of the weight-streaming entries."""
+    gu = randn(E, D, 2 * I, seed=seed, dtype=dtype, scale=scale).cuda()
+    dn = randn(E, I, D, seed=seed + 1, dtype=dtype, scale=scale).cuda()
+    return gu[..., :I].transpose(1, 2), gu[..., I:].transpose(1, 2), dn.transpose(1, 2)
+
+
+# GEMM tile entries 20 and 21: the weight-streaming tile with 16- / 32-row m-tiles (biops.h).
+STREAM_ENTRIES = (20, 21)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("T,E,D,I,k", [
+    (5, 4, 192, 72, 2),    # gate/up K = 192 (last stage of one 64-element step), N = 72 (partial block)
+    (6, 5, 64, 192, 3),    # gate/up K = 64; down K = 192, N = 64
+    (40, 3, 128, 64, 2),   # about 27 rows per expert: two 16-row m-tiles per group
+    (1, 64, 256, 136, 8),  # one token on eight experts
+])
+def test_stream_entries_equal_dense(dtype, T, E, D, I, k):
+    """The weight-streaming entries (automatic for few rows per expert, and forced) give the
+    dense path's bits on N-major weights, across partial column blocks, K tails and groups
+    taller than one m-tile."""
+    hidden = randn(T, D, seed=7700 + T, dtype=dtype).cuda()
+    gate, up, down = nmajor_weights(E, I, D, 7710 + E, dtype)
+    g = torch.Generator().manual_seed(7720 + T)
+    sel = torch.randint(0, E, (T, k), generator=g).cuda()
+    w = torch.rand(T, k, generator=g).cuda()
+    lib = nat.load()
+    dense = _moe(hidden, w, sel, gate, up, down, sparse=False)
+    try:
+        for cfg in (-1,) + STREAM_ENTRIES:
+            assert lib.biops_set_gemm_tile(cfg) == 0
+            sparse = _moe(hidden, w, sel, gate, up, down, sparse=True)
+            assert_bitwise(sparse, dense, f"tile entry {cfg}")
+    finally:
+        lib.biops_set_gemm_tile(-1)
+
+
+@pytest.mark.parametrize("T,E,k", [(128, 64, 8), (129, 64, 8), (3, 511, 4), (3, 512, 4)])
+def test_one_workgroup_packing_limits(monkeypatch, T, E, k):
+    """Up to 1024 routes and 511 experts the routes are packed by one workgroup, beyond by the
+    rank / plan / route-row kernels: both sides of each limit give the dense path's bits,
+    with an out-of-range index among the routes."""
+    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
+    D, I = 64, 64
+    hidden = randn(T, D, seed=7740 + T, dtype=torch.bfloat16).cuda()
+    gate, up, down = nmajor_weights(E, I, D, 7741, torch.bfloat16)
+    g = torch.Generator().manual_seed(7742 + E)
+    sel = torch.randint(0, E, (T, k), generator=g)
+    sel[T - 1, k - 1] = E
+    sel = sel.cuda()
+    w = torch.rand(T, k, generator=g).cuda()
+    dense, sparse = both(hidden, w, sel, gate, up, down)
+    assert_bitwise(sparse, dense, f"T={T} E={E}")
+    assert torch.count_nonzero(sparse[T - 1]) == 0
+    assert torch.count_nonzero(sparse[0]) > 0
