@@ -411,7 +411,7 @@ static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
 // eighth of the tiles; the tiles are numbered column-block-major, so the m-tiles of one group
 // and column block (the same weights) fall on one XCD and its L2.
 template <typename T, int BM, bool SWIGLU>
-__global__ __launch_bounds__(256) void stream_kernel(BmmArgs args) {
+__global__ __launch_bounds__((StreamTile<T, BM, SWIGLU>::THREADS)) void stream_kernel(BmmArgs args) {
   using S = StreamTile<T, BM, SWIGLU>;
   __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
   const uint32_t J = (uint32_t)args.grp[0];
@@ -449,7 +449,8 @@ static int launch_stream(const BmmArgs& a0, hipStream_t stream) {
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int64_t grid = (a.total + 7) & ~int64_t(7);
-  hipLaunchKernelGGL((stream_kernel<T, BM, SWIGLU>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((stream_kernel<T, BM, SWIGLU>), dim3((unsigned)grid),
+                     dim3(StreamTile<T, BM, SWIGLU>::THREADS), 0, stream, a);
   return check_launch("stream_kernel");
 }
 

@@ -12,12 +12,15 @@
 //
 // Arithmetic: v_mfma_f32_16x16x32 on 16-row x 16-column blocks, quad q' of a 128-byte K step
 // feeding chunks 4q'..4q'+3 (the chain of the skinny entry, gemm_skinny.h, whose bits equal
-// those of the two 32x32x16 pair steps of every other entry), K in order, no split.  Wavefront w
-// owns output columns 16w..16w+15 (gate and up accumulators of one output in the same lane);
-// the store rounds straight from the accumulators as the LDS-staged epilogues do.
+// those of the two 32x32x16 pair steps of every other entry), K in order, no split.  Plain:
+// four wavefronts, wavefront w owns output columns 16w..16w+15.  SwiGLU: eight wavefronts,
+// wavefront w owns the gate (w < 4) or up (w >= 4) columns 16(w%4)..+15, which halves each
+// wavefront's work per stage (one-token gate/up GEMM of 8 experts: 14.7 -> 11.8 us); after the
+// K loop the up wavefronts pass their accumulators through LDS to the gate wavefront of the
+// same columns.  The store rounds straight from the accumulators as the LDS-staged epilogues do.
 //
 // Operands go global -> LDS by global_load_lds_dwordx4 into a ring of 128-element K stages;
-// all four wavefronts load and compute (64-element stages and a 3-stage ring were measured
+// all wavefronts load and compute (64-element stages and a 3-stage ring were measured
 // slower for the gate/up GEMM: 16.6 and 16.5 us against 15.4 us before the batched reads).  A stage holds BM rows of A (K-major, 256 bytes each,
 // chunk c of row r in slot c ^ (r & 15)) and 128 K rows of B (N-major, the block's chunks of
 // 8 columns, gate then up, chunk pairs swizzled by K row), read back with ds_read_b128 (A) and
@@ -36,14 +39,18 @@ template <typename T, int BM, bool SWIGLU>
 struct StreamTile {
   static_assert(sizeof(T) == 2, "16-bit operands");
   static_assert(BM == 16 || BM == 32, "m-tile rows");
-  static constexpr int THREADS = 256;
+  static constexpr int THREADS = SWIGLU ? 512 : 256;
   static constexpr int OUT = 64;                          // output columns of a block
   static constexpr int CPR = (SWIGLU ? 2 : 1) * OUT / 8;  // 16-byte chunks of a B K row (8 / 16)
   static constexpr int SK = 128;                          // K elements of a stage
   static constexpr int STEPS = SK / 64;                   // 128-byte K steps of a stage
   static constexpr int RB = BM / 16;                      // 16-row MFMA blocks
   static constexpr int A_ROW = SK * 2;                    // bytes of one A row in a stage
-  static constexpr int LDS_A = BM * A_ROW;
+  // A slots of a stage; with fewer slots than threads the other threads load a copy of them
+  // into a spare area, so that every thread issues the same loads (constant vmcnt waits).
+  static constexpr int A_SLOTS = BM * (A_ROW / 16);
+  static constexpr int A_SPARE = A_SLOTS < THREADS ? (THREADS - A_SLOTS) * 16 : 0;
+  static constexpr int LDS_A = BM * A_ROW + A_SPARE;
   static constexpr int LDS_B = SK * CPR * 16;
   static constexpr int LDS_STAGE = LDS_A + LDS_B;
   // SwiGLU: as deep as 160 KiB allows (4 stages).  Plain: at most 4 stages within 80 KiB, so
@@ -52,10 +59,10 @@ struct StreamTile {
   static constexpr int STAGES_FIT = (SWIGLU ? 160 * 1024 : 80 * 1024) / LDS_STAGE;
   static constexpr int STAGES = STAGES_FIT < (SWIGLU ? 8 : 4) ? STAGES_FIT : (SWIGLU ? 8 : 4);
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
-  static constexpr int A_LOADS = BM * (A_ROW / 16) / THREADS;  // per thread and stage
+  static constexpr int A_LOADS = A_SLOTS < THREADS ? 1 : A_SLOTS / THREADS;  // per thread and stage
   static constexpr int B_LOADS = SK * CPR / THREADS;
   static constexpr int LOADS = A_LOADS + B_LOADS;
-  static_assert(A_LOADS * THREADS == BM * (A_ROW / 16) && B_LOADS * THREADS == SK * CPR, "load split");
+  static_assert((A_SLOTS < THREADS || A_LOADS * THREADS == A_SLOTS) && B_LOADS * THREADS == SK * CPR, "load split");
   static_assert(STAGES >= 3 && (STAGES - 1) * LOADS < 64, "ring depth and vmcnt range");
 
   // Chunk-pair swizzle of B K row k: the 16 rows one transposing read covers (k0 + 8g + i,
@@ -101,7 +108,8 @@ struct StreamTile {
     int64_t K;
   };
 
-  // The block over K (a multiple of 64).  Every wavefront returns its accumulators.
+  // The block over K (a multiple of 64).  Every wavefront returns its accumulators (SwiGLU:
+  // the gate wavefronts return gate and up of their columns).
   __device__ static __forceinline__ Acc run(char* smem, const Sources& S) {
     Acc acc;
 #pragma unroll
@@ -115,15 +123,15 @@ struct StreamTile {
     const int t = threadIdx.x;
     const int wbase = __builtin_amdgcn_readfirstlane(t & ~63);  // wave-uniform LDS offsets
 
-    // This thread's sources at K = 0.  A slot s = t + 256 p: row s / 16, slot s % 16 holding
-    // logical chunk (s % 16) ^ (row & 15).  B slot s = t + 256 p: K row s / CPR, slot s % CPR
+    // This thread's sources at K = 0.  A slot s = (t + THREADS p) % A_SLOTS: row s / 16, slot
+    // s % 16 holding logical chunk (s % 16) ^ (row & 15).  B slot s = t + THREADS p: K row s / CPR, slot s % CPR
     // holding logical chunk (s % CPR) ^ bswz(row); chunks past the last column re-load the last
     // whole chunk (never stored).
     const T* asrc[A_LOADS];
     int acol[A_LOADS];
 #pragma unroll
     for (int p = 0; p < A_LOADS; ++p) {
-      const int s = t + THREADS * p;
+      const int s = (t + THREADS * p) % A_SLOTS;
       const int r = s >> 4;
       const int c = (s & 15) ^ (r & 15);
       const int rr = r < S.rows ? r : S.rows - 1;
@@ -165,44 +173,34 @@ struct StreamTile {
 
     const int lane = t & 63, w = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
+    // Output column block jb of this wavefront, and the B part it reads (SwiGLU: 0 gate, 1 up).
+    const int jb = SWIGLU ? (w & 3) : w, part = SWIGLU ? (w >> 2) : 0;
     // Transposing reads: source lane lr points at K row 8 lg + lr / 4 (+ 4 for the upper half),
     // column 4 (lr % 4) of the wavefront's 16-column block.
-    const int tr_k = 8 * lg + (lr >> 2), tr_c = 16 * w + 4 * (lr & 3);
+    const int tr_k = 8 * lg + (lr >> 2), tr_c = OUT * part + 16 * jb + 4 * (lr & 3);
     // All fragment reads of a stage go out before one wait, then its MFMAs in K order (one
     // read latency per stage instead of one per K chunk: 15.4 -> 14.7 us for the one-token
-    // gate/up GEMM of 8 experts).
+    // gate/up GEMM of 8 experts).  The accumulator is acc.g in every wavefront.
     constexpr int KC = 2 * STEPS;  // 32-element K chunks of a stage
     auto compute = [&](const char* stage, int nsteps) {
       u32x4_t a[KC][RB];
-      u32x2_t glo[KC], ghi[KC], ulo[KC], uhi[KC];
+      u32x2_t blo[KC], bhi[KC];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
         for (int i = 0; i < RB; ++i)
           a[kc][i] = *reinterpret_cast<const u32x4_t*>(stage + a_off(16 * i + lr, 4 * kc + lg));
-        glo[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k, tr_c));
-        ghi[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k + 4, tr_c));
-        if constexpr (SWIGLU) {
-          ulo[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k, OUT + tr_c));
-          uhi[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k + 4, OUT + tr_c));
-        }
+        blo[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k, tr_c));
+        bhi[kc] = lds_read_tr16_asm(stage + b_off(32 * kc + tr_k + 4, tr_c));
       }
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        lds_wait_anchor(glo[kc], ghi[kc]);
-        if constexpr (SWIGLU) lds_wait_anchor(ulo[kc], uhi[kc]);
-      }
+      for (int kc = 0; kc < KC; ++kc) lds_wait_anchor(blo[kc], bhi[kc]);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
         if (kc >= 2 * nsteps) break;
-        const u32x4_t bg = u32x4_t{glo[kc][0], glo[kc][1], ghi[kc][0], ghi[kc][1]};
+        const u32x4_t bf = u32x4_t{blo[kc][0], blo[kc][1], bhi[kc][0], bhi[kc][1]};
 #pragma unroll
-        for (int i = 0; i < RB; ++i) Mfma16<T>::step(acc.g[i], a[kc][i], bg);
-        if constexpr (SWIGLU) {
-          const u32x4_t bu = u32x4_t{ulo[kc][0], ulo[kc][1], uhi[kc][0], uhi[kc][1]};
-#pragma unroll
-          for (int i = 0; i < RB; ++i) Mfma16<T>::step(acc.u[i], a[kc][i], bu);
-        }
+        for (int i = 0; i < RB; ++i) Mfma16<T>::step(acc.g[i], a[kc][i], bf);
       }
     };
 
@@ -221,14 +219,34 @@ struct StreamTile {
       compute(smem + (int)(s % STAGES) * LDS_STAGE, left < STEPS ? (int)left : STEPS);
     }
     wait_loads<0>();
+    if constexpr (SWIGLU) {
+      // The up wavefronts hand their accumulators to the gate wavefront of the same columns
+      // (acc.u there).  The ring is free: every load has landed and every read is done.
+      lds_barrier();
+      float* x = reinterpret_cast<float*>(smem);
+      if (part == 1) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x[((jb * RB + i) * 4 + r) * 64 + lane] = acc.g[i][r];
+      }
+      lds_barrier();
+      if (part == 0) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc.u[i][r] = x[((jb * RB + i) * 4 + r) * 64 + lane];
+      }
+    }
     return acc;
   }
 
-  // round(acc) (plain) or round(swiglu_value(gate, up)) of this lane's outputs: row
-  // 16 i + 4 (lane / 16) + r, column 16 w + lane % 16 of the block.
+  // round(acc) (plain) or round(swiglu_value(gate, up)) (the gate wavefronts) of this lane's
+  // outputs: row 16 i + 4 (lane / 16) + r, column 16 (w % 4) + lane % 16 of the block.
   __device__ static __forceinline__ void store(const Acc& acc, T* C, int64_t ldc, int rows, int64_t cols) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int col = 16 * w + (lane & 15);
+    if (SWIGLU && w >= 4) return;
+    const int col = 16 * (w & 3) + (lane & 15);
     if (col >= cols) return;
 #pragma unroll
     for (int i = 0; i < RB; ++i)
