@@ -65,10 +65,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   constexpr int V = 16 / (int)sizeof(T);
   constexpr int G = 8;
   const int64_t t = blockIdx.x;
+  // Every slot's index must be valid (the sparse path marks invalid ones with route row -1);
+  // the checks load G slots at a time, so that their latencies overlap.
   bool ok = true;
-  for (int64_t s = 0; s < a.k; ++s) {
-    const int64_t e = a.sel[t * a.k + s];
-    ok = ok && e >= 0 && e < a.E;
+  for (int64_t s0 = 0; s0 < a.k; s0 += G) {
+    int64_t v[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int64_t r = t * a.k + s0 + u;
+      v[u] = s0 + u < a.k ? (a.route_row ? (int64_t)a.route_row[r] : a.sel[r]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < G; ++u) ok = ok && (a.route_row ? v[u] >= 0 : (v[u] >= 0 && v[u] < a.E));
   }
   if (!ok && threadIdx.x == 0 && a.bad) *a.bad = 1;
   T* out = reinterpret_cast<T*>(a.out) + t * a.D;
@@ -136,13 +144,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
 
 // ------------------------------------------------------------------ route packing ----
 // Route r = t*k + s belongs to bucket sel[r] (an expert) or, for an index outside [0, E), to
-// bucket E (never computed).  The routes are cut into chunks of `chunk` consecutive routes:
+// bucket E (never computed).  The routes are cut into chunks of 64 consecutive routes, one
+// wavefront each:
 //   rank kernel  rank[r]      = routes r' < r of r's chunk in r's bucket,
-//                counts[c][b] = routes of chunk c in bucket b;
-//   plan kernel  counts[c][b] -> routes of chunks before c in bucket b (in place),
+//                counts[b][c] = routes of chunk c in bucket b (bucket-major);
+//   plan kernel  counts[b][c] -> routes of chunks before c in bucket b (in place; one
+//                wavefront scans a bucket's chunk counts 64 at a time),
 //                off[e]       = first packed row of expert e (experts in index order),
 //                grp1 / grp2  = m-tile tables of the two grouped GEMMs;
-//   route rows   row(r) = off[e] + counts[c][e] + rank[r]; row_token[row(r)] = t, the x row the
+//   route rows   row(r) = off[e] + counts[e][c] + rank[r]; row_token[row(r)] = t, the x row the
 //                gate/up GEMM reads for packed row row(r).
 // Packed rows of an expert are therefore its routes in increasing r.
 constexpr int kRankWaves = 4;
@@ -152,7 +162,7 @@ constexpr int kPlanThreads = 1024;
 struct PackArgs {
   const int64_t* sel;
   int32_t* rank;
-  int32_t* counts;     // [S][E + 1]
+  int32_t* counts;     // [E + 1][S]
   int32_t* off;        // [E + 1]
   int32_t* grp1;       // m-tiles of bm1 rows
   int32_t* grp2;       // m-tiles of bm2 rows
@@ -162,15 +172,11 @@ struct PackArgs {
   int32_t bm1, bm2;
 };
 
-static int64_t route_chunk(int64_t R) {
-  // 1024 routes per chunk, more when that gives over 256 chunks (the plan kernel walks them).
-  const int64_t batches = std::max<int64_t>(16, cdiv(R, int64_t(256) * 64));
-  return 64 * batches;
-}
+static int64_t route_chunk(int64_t) { return 64; }
 
-// One wavefront per chunk, 64 routes at a time: the lanes holding the same bucket find each
-// other through one ballot per bucket-index bit; each lane's rank is the count of such lanes
-// below it plus the bucket's running count, which the group's lowest lane advances.
+// One wavefront per chunk of 64 routes: the lanes holding the same bucket find each other
+// through one ballot per bucket-index bit; a lane's rank is the count of such lanes below it,
+// and the group's lowest lane records the group's size as the chunk's count of that bucket.
 __global__ __launch_bounds__(256) void moe_rank_kernel(PackArgs a) {
   extern __shared__ int32_t hist[];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -179,102 +185,142 @@ __global__ __launch_bounds__(256) void moe_rank_kernel(PackArgs a) {
   if (c >= a.S) return;  // whole wavefronts only; no workgroup barrier follows
   int32_t* h = hist + w * E1;
   for (int64_t b = lane; b < E1; b += 64) h[b] = 0;
-  const int nbits = 32 - __clz((int)a.E);
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  const int64_t r0 = c * a.chunk;
-  const int64_t r1 = std::min(a.R, r0 + a.chunk);
-  constexpr int NB = 16;  // batches of 64 routes whose selections are loaded together
-  for (int64_t base = r0; base < r1; base += 64 * NB) {
-    int bucket[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int64_t r = base + 64 * u + lane;
-      int b = (int)a.E;
-      if (r < r1) {
-        const int64_t e = a.sel[r];
-        if (e >= 0 && e < a.E) b = (int)e;
-      }
-      bucket[u] = b;
-    }
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int64_t r = base + 64 * u + lane;
-      const bool valid = r < r1;
-      const int b = bucket[u];
-      uint64_t same = __ballot(valid);
-      for (int bit = 0; bit < nbits; ++bit) {
-        const bool on = (b >> bit) & 1;
-        const uint64_t m = __ballot(valid && on);
-        same &= on ? m : ~m;
-      }
-      if (valid) {
-        const int32_t run = h[b];
-        const int lower = __popcll(same & below);
-        a.rank[r] = run + lower;
-        if (lower == 0) h[b] = run + __popcll(same);
-      }
-    }
+  const int64_t r = c * 64 + lane;
+  const bool valid = r < a.R;
+  int b = (int)a.E;
+  if (valid) {
+    const int64_t e = a.sel[r];
+    if (e >= 0 && e < a.E) b = (int)e;
   }
-  for (int64_t b = lane; b < E1; b += 64) a.counts[c * E1 + b] = h[b];
+  const int nbits = 32 - __clz((int)a.E);
+  uint64_t same = __ballot(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = (b >> bit) & 1;
+    const uint64_t m = __ballot(valid && on);
+    same &= on ? m : ~m;
+  }
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int lower = __popcll(same & below);
+  if (valid) {
+    a.rank[r] = lower;
+    if (lower == 0) h[b] = __popcll(same);
+  }
+  for (int64_t q = lane; q < E1; q += 64) a.counts[q * a.S + c] = h[q];
 }
 
-// One workgroup.  Thread i owns buckets [i*per, (i+1)*per); an exclusive scan over the threads
+// Workgroup barrier for data passed through LDS only: waits for this wavefront's LDS accesses,
+// not for its global stores (which a __syncthreads() waits for, and which no later step of
+// these kernels reads back).  The empty assembly statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// One workgroup.  First, wavefront w scans the chunk counts of buckets w, w + 16, ... (64 chunks
+// at a time, eight loads in flight) into routes of earlier chunks and records each bucket's
+// size.  Then thread i owns buckets [i*per, (i+1)*per), and a workgroup scan over the threads
 // of (rows, bm1 tiles, bm2 tiles) places each expert's rows and m-tiles.
 __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
-  __shared__ int32_t part[3][kPlanThreads];
-  const int tid = threadIdx.x;
+  constexpr int W = kPlanThreads / 64;
+  __shared__ int32_t size_l[kMaxSparseExperts + 1];
+  __shared__ int32_t wsum[W][3];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int64_t E = a.E, E1 = E + 1;
+  // Up to 512 chunks (32768 routes): the loads of NBK buckets of a wavefront go out together
+  // (the counts were just written by every XCD, so each load waits for memory).
+  constexpr int NBK = 8;
+  if (a.S <= 64 * 8) {
+    for (int64_t bb = w; bb < E1; bb += (int64_t)W * NBK) {
+      int32_t v[NBK][8];
+#pragma unroll
+      for (int j = 0; j < NBK; ++j) {
+        const int64_t b = bb + (int64_t)W * j;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t c = 64 * u + lane;
+          v[j][u] = (b < E1 && c < a.S) ? a.counts[b * a.S + c] : 0;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NBK; ++j) {
+        const int64_t b = bb + (int64_t)W * j;
+        if (b >= E1) break;
+        int32_t carry = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (64 * u >= a.S) break;
+          const int32_t inc = wave_incl_scan(v[j][u]);
+          const int64_t c = 64 * u + lane;
+          if (c < a.S) a.counts[b * a.S + c] = carry + inc - v[j][u];
+          carry += __shfl(inc, 63, 64);
+        }
+        if (lane == 0) size_l[b] = carry;
+      }
+    }
+  } else {
+    for (int64_t b = w; b < E1; b += W) {
+      int32_t carry = 0;
+      for (int64_t c0 = 0; c0 < a.S; c0 += 64 * 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t c = c0 + 64 * u + lane;
+          v[u] = c < a.S ? a.counts[b * a.S + c] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int32_t inc = wave_incl_scan(v[u]);
+          const int64_t c = c0 + 64 * u + lane;
+          if (c < a.S) a.counts[b * a.S + c] = carry + inc - v[u];
+          carry += __shfl(inc, 63, 64);
+        }
+      }
+      if (lane == 0) size_l[b] = carry;
+    }
+  }
+  lds_sync();
   const int64_t per = (E1 + kPlanThreads - 1) / kPlanThreads;
   const int64_t b0 = std::min(E1, tid * per), b1 = std::min(E1, b0 + per);
   int32_t rows = 0, t1 = 0, t2 = 0;
   for (int64_t b = b0; b < b1; ++b) {
-    int32_t run = 0;
-    int64_t c = 0;
-    for (; c + 4 <= a.S; c += 4) {
-      int32_t v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = a.counts[(c + u) * E1 + b];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        a.counts[(c + u) * E1 + b] = run;
-        run += v[u];
-      }
-    }
-    for (; c < a.S; ++c) {
-      const int32_t v = a.counts[c * E1 + b];
-      a.counts[c * E1 + b] = run;
-      run += v;
-    }
-    a.off[b] = run;  // bucket size for now
     if (b < E) {
-      rows += run;
-      t1 += (run + a.bm1 - 1) / a.bm1;
-      t2 += (run + a.bm2 - 1) / a.bm2;
+      const int32_t n = size_l[b];
+      rows += n;
+      t1 += (n + a.bm1 - 1) / a.bm1;
+      t2 += (n + a.bm2 - 1) / a.bm2;
     }
   }
-  part[0][tid] = rows;
-  part[1][tid] = t1;
-  part[2][tid] = t2;
-  __syncthreads();
-  // Inclusive Hillis-Steele scan over the threads.
-  for (int d = 1; d < kPlanThreads; d <<= 1) {
-    int32_t v0 = 0, v1 = 0, v2 = 0;
-    if (tid >= d) {
-      v0 = part[0][tid - d];
-      v1 = part[1][tid - d];
-      v2 = part[2][tid - d];
-    }
-    __syncthreads();
-    if (tid >= d) {
-      part[0][tid] += v0;
-      part[1][tid] += v1;
-      part[2][tid] += v2;
-    }
-    __syncthreads();
+  // exclusive scan over the threads: wavefront scans, then the sums of earlier wavefronts
+  const int32_t ir = wave_incl_scan(rows), i1 = wave_incl_scan(t1), i2 = wave_incl_scan(t2);
+  if (lane == 63) {
+    wsum[w][0] = ir;
+    wsum[w][1] = i1;
+    wsum[w][2] = i2;
   }
-  int32_t row0 = part[0][tid] - rows, j1 = part[1][tid] - t1, j2 = part[2][tid] - t2;
+  lds_sync();
+  int32_t pr = 0, p1 = 0, p2 = 0;
+  for (int v = 0; v < w; ++v) {
+    pr += wsum[v][0];
+    p1 += wsum[v][1];
+    p2 += wsum[v][2];
+  }
+  int32_t row0 = pr + ir - rows, j1 = p1 + i1 - t1, j2 = p2 + i2 - t2;
   for (int64_t b = b0; b < b1; ++b) {
-    const int32_t n = a.off[b];
+    const int32_t n = size_l[b];
     a.off[b] = row0;
     if (b < E) {
       for (int32_t m = 0; m < n; m += a.bm1, ++j1) {
@@ -288,9 +334,9 @@ __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
       row0 += n;
     }
   }
-  if (tid == 0) {
-    a.grp1[0] = part[1][kPlanThreads - 1];
-    a.grp2[0] = part[2][kPlanThreads - 1];
+  if (tid == kPlanThreads - 1) {
+    a.grp1[0] = p1 + i1;
+    a.grp2[0] = p2 + i2;
   }
 }
 
@@ -303,20 +349,9 @@ __global__ __launch_bounds__(256) void moe_route_rows_kernel(PackArgs a) {
   const int64_t e = a.sel[r];
   const bool ok = e >= 0 && e < a.E;
   int64_t row = -1;
-  if (ok) row = (int64_t)a.off[e] + a.counts[(r / a.chunk) * (a.E + 1) + e] + a.rank[r];
+  if (ok) row = (int64_t)a.off[e] + a.counts[e * a.S + r / a.chunk] + a.rank[r];
   a.route_row[r] = (int32_t)row;
   if (ok) a.row_token[row] = (int32_t)(r / a.k);
-}
-
-// Inclusive prefix sum over the 64 lanes of a wavefront.
-__device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  return v;
 }
 
 // Route packing of a small call in one workgroup: the rank, plan and route-row kernels above
@@ -353,7 +388,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
   const int lower = __popcll(same & below);
   // each wavefront writes only its own row of cnt (zeroed above by the same wavefront)
   if (valid && lower == 0) cnt[w][bucket] = __popcll(same);
-  __syncthreads();
+  lds_sync();
   int32_t n = 0;  // routes of bucket tid
   if (tid < E1) {
     for (int v = 0; v < kSmallPackWaves; ++v) {
@@ -372,7 +407,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
     wsum[w][1] = i1;
     wsum[w][2] = i2;
   }
-  __syncthreads();
+  lds_sync();
   int32_t pr = 0, p1 = 0, p2 = 0;
   for (int v = 0; v < w; ++v) {
     pr += wsum[v][0];
@@ -400,7 +435,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
     a.grp1[0] = p1 + i1;
     a.grp2[0] = p2 + i2;
   }
-  __syncthreads();
+  lds_sync();
   if (valid) {
     int32_t row = -1;
     if (bucket < E) {
