@@ -144,8 +144,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
 
 // ------------------------------------------------------------------ route packing ----
 // Route r = t*k + s belongs to bucket sel[r] (an expert) or, for an index outside [0, E), to
-// bucket E (never computed).  The routes are cut into chunks of 64 consecutive routes, one
-// wavefront each:
+// bucket E (never computed).  The routes are cut into chunks of 256 consecutive routes, one
+// workgroup each:
 //   rank kernel  rank[r]      = routes r' < r of r's chunk in r's bucket,
 //                counts[b][c] = routes of chunk c in bucket b (bucket-major);
 //   plan kernel  counts[b][c] -> routes of chunks before c in bucket b (in place; one
@@ -172,20 +172,31 @@ struct PackArgs {
   int32_t bm1, bm2;
 };
 
-static int64_t route_chunk(int64_t) { return 64; }
+static int64_t route_chunk(int64_t) { return 64 * kRankWaves; }
 
-// One wavefront per chunk of 64 routes: the lanes holding the same bucket find each other
-// through one ballot per bucket-index bit; a lane's rank is the count of such lanes below it,
-// and the group's lowest lane records the group's size as the chunk's count of that bucket.
+// Workgroup barrier for data passed through LDS only: waits for this wavefront's LDS accesses,
+// not for its global stores (which a __syncthreads() waits for, and which no later step of
+// these kernels reads back).  The empty assembly statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One workgroup per chunk of 256 routes, one wavefront per 64 of them: the lanes holding the
+// same bucket find each other through one ballot per bucket-index bit; a route's rank is the
+// count of such lanes below it plus the bucket's routes in the chunk's earlier wavefronts, and
+// the chunk's count of a bucket sums its four wavefronts' counts.
 __global__ __launch_bounds__(256) void moe_rank_kernel(PackArgs a) {
-  extern __shared__ int32_t hist[];
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  extern __shared__ int32_t hist[];  // [kRankWaves][E + 1]
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int64_t E1 = a.E + 1;
-  const int64_t c = (int64_t)blockIdx.x * kRankWaves + w;
-  if (c >= a.S) return;  // whole wavefronts only; no workgroup barrier follows
+  const int64_t c = blockIdx.x;
   int32_t* h = hist + w * E1;
   for (int64_t b = lane; b < E1; b += 64) h[b] = 0;
-  const int64_t r = c * 64 + lane;
+  const int64_t r = c * (64 * kRankWaves) + tid;
   const bool valid = r < a.R;
   int b = (int)a.E;
   if (valid) {
@@ -201,22 +212,19 @@ __global__ __launch_bounds__(256) void moe_rank_kernel(PackArgs a) {
   }
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int lower = __popcll(same & below);
+  if (valid && lower == 0) h[b] = __popcll(same);
+  lds_sync();
   if (valid) {
-    a.rank[r] = lower;
-    if (lower == 0) h[b] = __popcll(same);
+    int32_t before = 0;
+    for (int v = 0; v < w; ++v) before += hist[v * E1 + b];
+    a.rank[r] = before + lower;
   }
-  for (int64_t q = lane; q < E1; q += 64) a.counts[q * a.S + c] = h[q];
-}
-
-// Workgroup barrier for data passed through LDS only: waits for this wavefront's LDS accesses,
-// not for its global stores (which a __syncthreads() waits for, and which no later step of
-// these kernels reads back).  The empty assembly statements keep the compiler from moving
-// memory accesses across it.
-__device__ __forceinline__ void lds_sync() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt unchanged
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  for (int64_t q = tid; q < E1; q += 64 * kRankWaves) {
+    int32_t n = 0;
+#pragma unroll
+    for (int v = 0; v < kRankWaves; ++v) n += hist[v * E1 + q];
+    a.counts[q * a.S + c] = n;
+  }
 }
 
 // Inclusive prefix sum over the 64 lanes of a wavefront.
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
   __shared__ int32_t wsum[W][3];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int64_t E = a.E, E1 = E + 1;
-  // Up to 512 chunks (32768 routes): the loads of NBK buckets of a wavefront go out together
+  // Up to 512 chunks (131072 routes): the loads of NBK buckets of a wavefront go out together
   // (the counts were just written by every XCD, so each load waits for memory).
   constexpr int NBK = 8;
   if (a.S <= 64 * 8) {
@@ -655,7 +663,7 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
       if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
     } else {
       const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
-      hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)cdiv(p.S, kRankWaves)), dim3(256), hist_bytes, s, p);
+      hipLaunchKernelGGL(moe_rank_kernel, dim3((unsigned)p.S), dim3(64 * kRankWaves), hist_bytes, s, p);
       if ((rc = check_launch("moe_rank_kernel")) != BIOPS_OK) return rc;
       hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
       if ((rc = check_launch("moe_plan_kernel")) != BIOPS_OK) return rc;
