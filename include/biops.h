@@ -108,8 +108,8 @@ int biops_gemm_tile_count(void);
  * choice for fp32; entries 12 (one 32x32 block per workgroup with loader wavefronts, for few
  * rows) and 13-19 (blocks of 256x256, 256x128, 128x256, 128x128, 128x64, 64x128 and 64x64 on
  * four wavefronts, 16-bit types only) need K-major B, 16-byte aligned rows and K a multiple of
- * 128 bytes and fall back to the automatic choice elsewhere.  Entries 20 and 21 (the
- * weight-streaming tile: 16- or 32-row m-tiles x 64 output columns, for grouped rows with few
+ * 128 bytes and fall back to the automatic choice elsewhere.  Entries 20-22 (the
+ * weight-streaming tile: 16-, 32- or 64-row m-tiles x 64 output columns, for grouped rows with few
  * rows per group) serve only the MoE expert GEMMs with 16-bit N-major weights, 16-byte aligned
  * rows and K a multiple of 128 bytes, and fall back to the automatic choice elsewhere.
  * For tuning and for the cross-entry bitwise tests.  No reference counterpart. */

@@ -70,12 +70,12 @@ constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weigh
 // 0.96 on the shapes it wins).
 static const double kBigNmajorShare[kNumBig] = {0.93, 0.91, 0.87, 0.87, 0.88, 0.79, 0.86};
 constexpr int kBigEnd = kBigCfg + kNumBig;
-// Entries 20 and 21: the weight-streaming tile (gemm_stream.h), one m-tile of 16 (entry 20) or 32
-// (entry 21) rows x 64 output columns per workgroup.  Grouped rows with a 16-bit N-major B
-// only (the MoE expert GEMMs); elsewhere they fall back to the automatic choice.
+// Entries 20-22: the weight-streaming tile (gemm_stream.h), one m-tile of 16 (entry 20), 32
+// (entry 21) or 64 (entry 22) rows x 64 output columns per workgroup.  Grouped rows with a
+// 16-bit N-major B only (the MoE expert GEMMs); elsewhere they fall back to the automatic choice.
 constexpr int kStreamCfg = kBigEnd;
-constexpr int kNumStream = 2;
-static const int kStreamBM[kNumStream] = {16, 32};
+constexpr int kNumStream = 3;
+static const int kStreamBM[kNumStream] = {16, 32, 64};
 static_assert(kMinGroupedTileRows == 16, "grouped tables are sized for the 16-row stream entry");
 constexpr int kMenuSize = kStreamCfg + kNumStream;
 
@@ -371,13 +371,15 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // against 11.4).
   if ((best == 4 || best == 6) && prefer32) best = (big_ok && !nmajor16) ? kBigCfg + 6 : 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
-  // Grouped rows of at most 16 rows per group on average with a 16-bit N-major B (the MoE
-  // expert GEMMs of calls up to about 2E/k tokens): the weight-streaming entries.  MI355X, C5
+  // Grouped rows of at most 40 rows per group on average with a 16-bit N-major B (the MoE
+  // expert GEMMs of calls up to about 5E/k tokens): the weight-streaming entries.  MI355X, C5
   // shapes (E = 64, D = 2048, I = 768, top-8), per sparse MoE call against the best table entry:
   // 1 token 47.1 us (16 rows) against 62.8 (entry 7); 2 tokens 56.3 against 74.5 (entry 2);
-  // 32 tokens 154.6 (32 rows) against 171.4; 128 tokens 163.5 (32 rows) against 177.7; at 256
-  // tokens (32 rows per group) entry 2 wins, 180.1 against 207.2.
-  if (stream_ok && mean <= 16) best = mean <= 2 ? kStreamCfg : kStreamCfg + 1;
+  // 32 tokens 154.6 (32 rows) against 171.4; 128 tokens 130.5 (32 rows) against 160.9; 256
+  // tokens (32 rows per group) 160.1 (64 rows) against 170.8; at 384 tokens entry 2 wins,
+  // 175.2 against 182.3 (64 rows).
+  if (stream_ok && mean <= 40)
+    best = mean <= 2 ? kStreamCfg : mean <= 16 ? kStreamCfg + 1 : kStreamCfg + 2;
   return best;
 }
 
@@ -521,6 +523,9 @@ static int launch_grouped_typed(const BmmArgs& a, bool b_kmajor, bool direct, in
       break;
     case kStreamCfg + 1:
       if constexpr (sizeof(T) == 2) return launch_stream<T, 32, !kPlain>(a, s);
+      break;
+    case kStreamCfg + 2:
+      if constexpr (sizeof(T) == 2) return launch_stream<T, 64, !kPlain>(a, s);
       break;
     default: break;
   }

@@ -38,7 +38,7 @@ namespace biops {
 template <typename T, int BM, bool SWIGLU>
 struct StreamTile {
   static_assert(sizeof(T) == 2, "16-bit operands");
-  static_assert(BM == 16 || BM == 32, "m-tile rows");
+  static_assert(BM == 16 || BM == 32 || BM == 64, "m-tile rows");
   static constexpr int THREADS = SWIGLU ? 512 : 256;
   static constexpr int OUT = 64;                          // output columns of a block
   static constexpr int CPR = (SWIGLU ? 2 : 1) * OUT / 8;  // 16-byte chunks of a B K row (8 / 16)
@@ -53,10 +53,12 @@ struct StreamTile {
   static constexpr int LDS_A = BM * A_ROW + A_SPARE;
   static constexpr int LDS_B = SK * CPR * 16;
   static constexpr int LDS_STAGE = LDS_A + LDS_B;
-  // SwiGLU: as deep as 160 KiB allows (4 stages).  Plain: at most 4 stages within 80 KiB, so
-  // that two workgroups share a compute unit: the down GEMM of 64 one-row groups (K = 768)
-  // took 48.5 us with an 8-stage ring and 31.0 us with 4, of 8 groups 6.4 and 5.6 us (MI355X).
-  static constexpr int STAGES_FIT = (SWIGLU ? 160 * 1024 : 80 * 1024) / LDS_STAGE;
+  // SwiGLU: as deep as 160 KiB allows (4 stages; 3 with 64-row m-tiles).  Plain: at most 4
+  // stages within 80 KiB, so that two workgroups share a compute unit (the down GEMM of 64
+  // one-row groups, K = 768, took 48.5 us with an 8-stage ring and 31.0 us with 4, of 8 groups
+  // 6.4 and 5.6 us, MI355X); with 64-row m-tiles, whose stages are twice as large, 4 stages in
+  // 160 KiB.
+  static constexpr int STAGES_FIT = (SWIGLU || BM == 64 ? 160 * 1024 : 80 * 1024) / LDS_STAGE;
   static constexpr int STAGES = STAGES_FIT < (SWIGLU ? 8 : 4) ? STAGES_FIT : (SWIGLU ? 8 : 4);
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
   static constexpr int A_LOADS = A_SLOTS < THREADS ? 1 : A_SLOTS / THREADS;  // per thread and stage

@@ -181,8 +181,8 @@ def nmajor_weights(E, I, D, seed, dtype, scale=0.1):
     return gu[..., :I].transpose(1, 2), gu[..., I:].transpose(1, 2), dn.transpose(1, 2)
 
 
-# GEMM tile entries 20 and 21: the weight-streaming tile with 16- / 32-row m-tiles (biops.h).
-STREAM_ENTRIES = (20, 21)
+# GEMM tile entries 20-22: the weight-streaming tile with 16- / 32- / 64-row m-tiles (biops.h).
+STREAM_ENTRIES = (20, 21, 22)
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
