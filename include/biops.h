@@ -342,7 +342,7 @@ int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
  * made; the array's device address is looked up once per device (hipGetSymbolAddress, with that
  * device current).  Sizes whose biops_moe_sparse_workspace_size exceeds the array return
  * BIOPS_ERR_SIZE before any GPU work (C5 shapes -- hidden 2048, intermediate 768, top-8 -- fit up
- * to 1484 tokens).  The stream must belong to the current device.  Every call on one GPU uses
+ * to 1485 tokens).  The stream must belong to the current device.  Every call on one GPU uses
  * the same array: calls that overlap on one GPU (two streams, or two host threads) race and must
  * be serialised by the caller.  Nothing in the array needs to start at zero: each call writes
  * every table before reading it.

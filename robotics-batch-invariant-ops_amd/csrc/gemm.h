@@ -52,6 +52,16 @@ int launch_bmm(int dtype, BmmArgs a, int epi, bool b_kmajor, hipStream_t stream)
 // size (0 on error).
 int grouped_tile_rows(int dtype, BmmArgs a, int epi, bool b_kmajor);
 
+// Tail m-tiles of a grouped problem: when the entry launch_bmm picks has m-tiles of 128 rows or
+// more, the groups hold at least two such m-tiles on average and B is a 16-bit N-major matrix
+// on the direct path, a group's last m-tile with fewer rows than the returned count is better
+// run apart, on the weight-streaming tile (one such sliver in a 256-row tile costs a whole
+// tile); 0 when the problem has no such split.
+int grouped_tail_rows(int dtype, BmmArgs a, int epi, bool b_kmajor);
+// The tail m-tiles listed in a.grp (m-tiles of up to grouped_tail_rows() rows) on the
+// weight-streaming tile; same bits as any other entry.
+int launch_grouped_tail(int dtype, BmmArgs a, int epi, hipStream_t stream);
+
 // Packed variable-length attention work list (host and device copies share the layout):
 //   plan[0] items, plan[1] QK^T tiles, plan[2] PV tiles, plan[3] score rows,
 //   plan[4] score elements, plan[5..7] reserved,

@@ -151,7 +151,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
 //   plan kernel  counts[b][c] -> routes of chunks before c in bucket b (in place; one
 //                wavefront scans a bucket's chunk counts 64 at a time),
 //                off[e]       = first packed row of expert e (experts in index order),
-//                grp1 / grp2  = m-tile tables of the two grouped GEMMs;
+//                grp1 / grp2  = m-tile tables of the two grouped GEMMs (with tail1 / tail2 > 0
+//                               an expert's last m-tile of fewer rows goes to grp1t / grp2t,
+//                               the tables of the tail launches);
 //   route rows   row(r) = off[e] + counts[e][c] + rank[r]; row_token[row(r)] = t, the x row the
 //                gate/up GEMM reads for packed row row(r).
 // Packed rows of an expert are therefore its routes in increasing r.
@@ -166,10 +168,13 @@ struct PackArgs {
   int32_t* off;        // [E + 1]
   int32_t* grp1;       // m-tiles of bm1 rows
   int32_t* grp2;       // m-tiles of bm2 rows
+  int32_t* grp1t;      // tail m-tiles of the gate/up GEMM (tail1 > 0; plan kernel only)
+  int32_t* grp2t;      // tail m-tiles of the down GEMM (tail2 > 0; plan kernel only)
   int32_t* route_row;  // [R], -1 for bucket E
   int32_t* row_token;  // [R] token of each packed row
   int64_t R, k, E, S, chunk;
   int32_t bm1, bm2;
+  int32_t tail1, tail2;  // rows below which an expert's last m-tile is a tail (0: none)
 };
 
 static int64_t route_chunk(int64_t) { return 64 * kRankWaves; }
@@ -241,11 +246,11 @@ __device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
 // One workgroup.  First, wavefront w scans the chunk counts of buckets w, w + 16, ... (64 chunks
 // at a time, eight loads in flight) into routes of earlier chunks and records each bucket's
 // size.  Then thread i owns buckets [i*per, (i+1)*per), and a workgroup scan over the threads
-// of (rows, bm1 tiles, bm2 tiles) places each expert's rows and m-tiles.
+// of (rows, main and tail m-tiles of both GEMMs) places each expert's rows and m-tiles.
 __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
   constexpr int W = kPlanThreads / 64;
   __shared__ int32_t size_l[kMaxSparseExperts + 1];
-  __shared__ int32_t wsum[W][3];
+  __shared__ int32_t wsum[W][5];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int64_t E = a.E, E1 = E + 1;
   // Up to 512 chunks (131072 routes): the loads of NBK buckets of a wavefront go out together
@@ -303,48 +308,63 @@ __global__ __launch_bounds__(kPlanThreads) void moe_plan_kernel(PackArgs a) {
   lds_sync();
   const int64_t per = (E1 + kPlanThreads - 1) / kPlanThreads;
   const int64_t b0 = std::min(E1, tid * per), b1 = std::min(E1, b0 + per);
-  int32_t rows = 0, t1 = 0, t2 = 0;
+  // m-tiles of an expert of n rows in a table of bm-row tiles: main ones, and whether the last
+  // one (fewer than `tail` rows) is a tail
+  auto tiles = [](int32_t n, int32_t bm, int32_t tail, int32_t& main, int32_t& tl) {
+    const int32_t all = (n + bm - 1) / bm;
+    tl = (all > 0 && n - (all - 1) * bm < tail) ? 1 : 0;
+    main = all - tl;
+  };
+  // per thread: rows, gate/up main and tail m-tiles, down main and tail m-tiles
+  int32_t q[5] = {0, 0, 0, 0, 0};
   for (int64_t b = b0; b < b1; ++b) {
     if (b < E) {
       const int32_t n = size_l[b];
-      rows += n;
-      t1 += (n + a.bm1 - 1) / a.bm1;
-      t2 += (n + a.bm2 - 1) / a.bm2;
+      int32_t m1, x1, m2, x2;
+      tiles(n, a.bm1, a.tail1, m1, x1);
+      tiles(n, a.bm2, a.tail2, m2, x2);
+      q[0] += n; q[1] += m1; q[2] += x1; q[3] += m2; q[4] += x2;
     }
   }
   // exclusive scan over the threads: wavefront scans, then the sums of earlier wavefronts
-  const int32_t ir = wave_incl_scan(rows), i1 = wave_incl_scan(t1), i2 = wave_incl_scan(t2);
-  if (lane == 63) {
-    wsum[w][0] = ir;
-    wsum[w][1] = i1;
-    wsum[w][2] = i2;
+  int32_t inc[5], pre[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    inc[i] = wave_incl_scan(q[i]);
+    if (lane == 63) wsum[w][i] = inc[i];
   }
   lds_sync();
-  int32_t pr = 0, p1 = 0, p2 = 0;
-  for (int v = 0; v < w; ++v) {
-    pr += wsum[v][0];
-    p1 += wsum[v][1];
-    p2 += wsum[v][2];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    pre[i] = 0;
+    for (int v = 0; v < w; ++v) pre[i] += wsum[v][i];
   }
-  int32_t row0 = pr + ir - rows, j1 = p1 + i1 - t1, j2 = p2 + i2 - t2;
+  int32_t row0 = pre[0] + inc[0] - q[0];
+  int32_t j1 = pre[1] + inc[1] - q[1], k1 = pre[2] + inc[2] - q[2];
+  int32_t j2 = pre[3] + inc[3] - q[3], k2 = pre[4] + inc[4] - q[4];
+  auto put = [](int32_t* table, int32_t j, int32_t e, int32_t first, int32_t end) {
+    int32_t* g = table + kGrpHeader + kGrpStride * j;
+    g[0] = e; g[1] = first; g[2] = end; g[3] = 0;
+  };
   for (int64_t b = b0; b < b1; ++b) {
     const int32_t n = size_l[b];
     a.off[b] = row0;
     if (b < E) {
-      for (int32_t m = 0; m < n; m += a.bm1, ++j1) {
-        int32_t* g = a.grp1 + kGrpHeader + kGrpStride * j1;
-        g[0] = (int32_t)b; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
-      }
-      for (int32_t m = 0; m < n; m += a.bm2, ++j2) {
-        int32_t* g = a.grp2 + kGrpHeader + kGrpStride * j2;
-        g[0] = (int32_t)b; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
-      }
+      int32_t m1, x1, m2, x2;
+      tiles(n, a.bm1, a.tail1, m1, x1);
+      tiles(n, a.bm2, a.tail2, m2, x2);
+      for (int32_t t = 0; t < m1; ++t) put(a.grp1, j1++, (int32_t)b, row0 + t * a.bm1, row0 + n);
+      if (x1) put(a.grp1t, k1++, (int32_t)b, row0 + m1 * a.bm1, row0 + n);
+      for (int32_t t = 0; t < m2; ++t) put(a.grp2, j2++, (int32_t)b, row0 + t * a.bm2, row0 + n);
+      if (x2) put(a.grp2t, k2++, (int32_t)b, row0 + m2 * a.bm2, row0 + n);
       row0 += n;
     }
   }
   if (tid == kPlanThreads - 1) {
-    a.grp1[0] = p1 + i1;
-    a.grp2[0] = p2 + i2;
+    a.grp1[0] = pre[1] + inc[1];
+    a.grp2[0] = pre[3] + inc[3];
+    if (a.tail1 > 0) a.grp1t[0] = pre[2] + inc[2];
+    if (a.tail2 > 0) a.grp2t[0] = pre[4] + inc[4];
   }
 }
 
@@ -456,7 +476,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
 
 // Workspace of the sparse path (byte offsets, 256-byte aligned).
 struct SparseLayout {
-  int64_t y, act, rank, route, token, counts, off, grp1, grp2, total;
+  int64_t y, act, rank, route, token, counts, off, grp1, grp2, grp1t, grp2t, total;
 };
 
 static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int64_t I) {
@@ -475,6 +495,9 @@ static SparseLayout sparse_layout(int elt, int64_t R, int64_t E, int64_t D, int6
   L.off = p; p += al((E + 1) * 4);
   L.grp1 = p; p += al((kGrpHeader + kGrpStride * tiles) * 4);
   L.grp2 = p; p += al((kGrpHeader + kGrpStride * tiles) * 4);
+  // tail tables: at most one m-tile per expert
+  L.grp1t = p; p += al((kGrpHeader + kGrpStride * std::min(E, R)) * 4);
+  L.grp2t = p; p += al((kGrpHeader + kGrpStride * std::min(E, R)) * 4);
   L.total = p;
   return L;
 }
@@ -658,7 +681,13 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
     p.chunk = route_chunk(R);
     p.S = cdiv(R, p.chunk);
     p.bm1 = bm1; p.bm2 = bm2;
-    if (R <= kSmallPackRoutes && experts + 1 <= kSmallPackBuckets) {
+    p.grp1t = reinterpret_cast<int32_t*>(ws + L.grp1t);
+    p.grp2t = reinterpret_cast<int32_t*>(ws + L.grp2t);
+    const bool small = R <= kSmallPackRoutes && experts + 1 <= kSmallPackBuckets;
+    // Tail m-tiles go to separate launches on the weight-streaming tile (plan kernel path).
+    p.tail1 = small ? 0 : grouped_tail_rows(dtype, g.gu, kEpiSwiglu, g.gu_kmajor);
+    p.tail2 = small ? 0 : grouped_tail_rows(dtype, g.dn, kEpiPlain, g.dn_kmajor);
+    if (small) {
       hipLaunchKernelGGL(moe_pack_small_kernel, dim3(1), dim3(kSmallPackRoutes), 0, s, p);
       if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
     } else {
@@ -670,8 +699,18 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
       hipLaunchKernelGGL(moe_route_rows_kernel, dim3((unsigned)cdiv(R, 256)), dim3(256), 0, s, p);
       if ((rc = check_launch("moe_route_rows_kernel")) != BIOPS_OK) return rc;
     }
+    // the tail launches: at most one m-tile per expert
+    auto tail_of = [&](BmmArgs t, int32_t* table) {
+      t.grp = table;
+      t.grp_rows = t.grp_groups = std::min<int64_t>(R, experts);
+      return t;
+    };
     if ((rc = launch_bmm(dtype, g.gu, kEpiSwiglu, g.gu_kmajor, s)) != BIOPS_OK) return rc;
+    if (p.tail1 > 0 && (rc = launch_grouped_tail(dtype, tail_of(g.gu, p.grp1t), kEpiSwiglu, s)) != BIOPS_OK)
+      return rc;
     if ((rc = launch_bmm(dtype, g.dn, kEpiPlain, g.dn_kmajor, s)) != BIOPS_OK) return rc;
+    if (p.tail2 > 0 && (rc = launch_grouped_tail(dtype, tail_of(g.dn, p.grp2t), kEpiPlain, s)) != BIOPS_OK)
+      return rc;
   }
   CombineArgs c{ws + L.y, weights, sel, route_row, out, bad_index, tokens, hidden, experts, top_k, w_dtype, 0};
   return launch_combine(dtype, c, s);

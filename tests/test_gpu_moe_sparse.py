@@ -232,3 +232,26 @@ def test_one_workgroup_packing_limits(monkeypatch, T, E, k):
     if T > 1:
         assert torch.count_nonzero(sparse[T - 1]) == 0
     assert torch.count_nonzero(sparse[0]) > 0
+
+
+@pytest.mark.parametrize("cfg", (-1, 0, 2))
+def test_tail_m_tiles_equal_dense(cfg):
+    """Groups of two m-tiles or more (here 530 / 600 / 520 / 700 rows on N-major weights): an
+    expert's last m-tile of fewer than 64 rows runs as a separate launch on the
+    weight-streaming tile, with the dense path's bits (256- and 128-row main tiles)."""
+    sizes = (530, 600, 520, 700)
+    E, D, I = len(sizes), 128, 128
+    T = sum(sizes)
+    sel = torch.cat([torch.full((n,), e, dtype=torch.int64) for e, n in enumerate(sizes)])
+    sel = sel[torch.randperm(T, generator=torch.Generator().manual_seed(7760))].reshape(T, 1).cuda()
+    w = torch.rand(T, 1, generator=torch.Generator().manual_seed(7761)).cuda()
+    hidden = randn(T, D, seed=7762, dtype=torch.bfloat16).cuda()
+    gate, up, down = nmajor_weights(E, I, D, 7763, torch.bfloat16)
+    lib = nat.load()
+    dense = _moe(hidden, w, sel, gate, up, down, sparse=False)
+    try:
+        assert lib.biops_set_gemm_tile(cfg) == 0
+        sparse = _moe(hidden, w, sel, gate, up, down, sparse=True)
+    finally:
+        lib.biops_set_gemm_tile(-1)
+    assert_bitwise(sparse, dense, f"tile entry {cfg}")
