@@ -20,11 +20,11 @@
 // same columns.  The store rounds straight from the accumulators as the LDS-staged epilogues do.
 //
 // Operands go global -> LDS by global_load_lds_dwordx4 into a ring of 128-element K stages;
-// all wavefronts load and compute (64-element stages and a 3-stage ring were measured
-// slower for the gate/up GEMM: 16.6 and 16.5 us against 15.4 us before the batched reads).  A stage holds BM rows of A (K-major, 256 bytes each,
-// chunk c of row r in slot c ^ (r & 15)) and 128 K rows of B (N-major, the block's chunks of
-// 8 columns, gate then up, chunk pairs swizzled by K row), read back with ds_read_b128 (A) and
-// the transposing ds_read_b64_tr_b16 (B).
+// all wavefronts load and compute (64-element stages and a 3-stage ring were measured slower
+// for the gate/up GEMM: 16.6 and 16.5 us against 15.4 us before the batched reads).  A stage
+// holds BM rows of A (K-major, 256 bytes each, chunk c of row r in slot c ^ (r & 15)) and 128 K
+// rows of B (N-major, the block's chunks of 8 columns, gate then up, chunk pairs swizzled by K
+// row), read back with ds_read_b128 (A) and the transposing ds_read_b64_tr_b16 (B).
 //
 // Requirements (checked by the launcher): 16-bit types, grouped rows, N-major B with 16-byte
 // aligned rows and N a multiple of 8, K a multiple of 64.
@@ -64,7 +64,8 @@ struct StreamTile {
   static constexpr int A_LOADS = A_SLOTS < THREADS ? 1 : A_SLOTS / THREADS;  // per thread and stage
   static constexpr int B_LOADS = SK * CPR / THREADS;
   static constexpr int LOADS = A_LOADS + B_LOADS;
-  static_assert((A_SLOTS < THREADS || A_LOADS * THREADS == A_SLOTS) && B_LOADS * THREADS == SK * CPR, "load split");
+  static_assert((A_SLOTS < THREADS || A_LOADS * THREADS == A_SLOTS) && B_LOADS * THREADS == SK * CPR,
+                "load split");
   static_assert(STAGES >= 3 && (STAGES - 1) * LOADS < 64, "ring depth and vmcnt range");
 
   // Chunk-pair swizzle of B K row k: the 16 rows one transposing read covers (k0 + 8g + i,
@@ -126,9 +127,9 @@ struct StreamTile {
     const int wbase = __builtin_amdgcn_readfirstlane(t & ~63);  // wave-uniform LDS offsets
 
     // This thread's sources at K = 0.  A slot s = (t + THREADS p) % A_SLOTS: row s / 16, slot
-    // s % 16 holding logical chunk (s % 16) ^ (row & 15).  B slot s = t + THREADS p: K row s / CPR, slot s % CPR
-    // holding logical chunk (s % CPR) ^ bswz(row); chunks past the last column re-load the last
-    // whole chunk (never stored).
+    // s % 16 holding logical chunk (s % 16) ^ (row & 15).  B slot s = t + THREADS p: K row
+    // s / CPR, slot s % CPR holding logical chunk (s % CPR) ^ bswz(row); chunks past the last
+    // column re-load the last whole chunk (never stored).
     const T* asrc[A_LOADS];
     int acol[A_LOADS];
 #pragma unroll
