@@ -66,17 +66,30 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   constexpr int G = 8;
   const int64_t t = blockIdx.x;
   // Every slot's index must be valid (the sparse path marks invalid ones with route row -1);
-  // the checks load G slots at a time, so that their latencies overlap.
+  // the checks load G slots at a time, so that their latencies overlap.  The y rows and
+  // routing weights of the first G slots (every slot for k <= G) are kept for the sums below,
+  // together with those loads.
   bool ok = true;
+  int64_t row0[G];
+  float w0[G];
   for (int64_t s0 = 0; s0 < a.k; s0 += G) {
     int64_t v[G];
+    float wv[G];
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       const int64_t r = t * a.k + s0 + u;
       v[u] = s0 + u < a.k ? (a.route_row ? (int64_t)a.route_row[r] : a.sel[r]) : 0;
+      wv[u] = s0 + u < a.k ? load_weight<T>(a.w, a.w_dtype, r) : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < G; ++u) ok = ok && (a.route_row ? v[u] >= 0 : (v[u] >= 0 && v[u] < a.E));
+    if (s0 == 0) {
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        row0[u] = a.route_row ? v[u] : v[u] * a.T + t;
+        w0[u] = wv[u];
+      }
+    }
   }
   if (!ok && threadIdx.x == 0 && a.bad) *a.bad = 1;
   T* out = reinterpret_cast<T*>(a.out) + t * a.D;
@@ -97,8 +110,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
           for (int u = 0; u < G; ++u) {
             if (s0 + u < a.k) {
               const int64_t r = t * a.k + s0 + u;
-              w[u] = load_weight<T>(a.w, a.w_dtype, r);
-              v[u] = *reinterpret_cast<const u32x4_t*>(ybase + row_of(r) * a.D + d0);
+              w[u] = s0 == 0 ? w0[u] : load_weight<T>(a.w, a.w_dtype, r);
+              const int64_t row = s0 == 0 ? row0[u] : row_of(r);
+              v[u] = *reinterpret_cast<const u32x4_t*>(ybase + row * a.D + d0);
             }
           }
 #pragma unroll
