@@ -255,3 +255,22 @@ def test_tail_m_tiles_equal_dense(cfg):
     finally:
         lib.biops_set_gemm_tile(-1)
     assert_bitwise(sparse, dense, f"tile entry {cfg}")
+
+
+def test_plan_over_512_chunks(monkeypatch):
+    """Over 131072 routes (more than 512 chunks of 256) the plan kernel scans each expert's
+    chunk counts in several passes; the sparse path still gives the dense path's bits, with
+    out-of-range indices among the routes."""
+    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
+    T, E, D, I, k = 70000, 5, 64, 64, 2
+    hidden = randn(T, D, seed=7770, dtype=torch.bfloat16).cuda()
+    gate, up, down = nmajor_weights(E, I, D, 7771, torch.bfloat16)
+    g = torch.Generator().manual_seed(7772)
+    sel = torch.randint(0, E, (T, k), generator=g)
+    sel[12345, 1] = E
+    sel[T - 1, 0] = -3
+    sel = sel.cuda()
+    w = torch.rand(T, k, generator=g).cuda()
+    dense, sparse = both(hidden, w, sel, gate, up, down)
+    assert_bitwise(sparse, dense, "140000 routes")
+    assert torch.count_nonzero(sparse[12345]) == 0 and torch.count_nonzero(sparse[T - 1]) == 0
