@@ -86,7 +86,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
     if (s0 == 0) {
 #pragma unroll
       for (int u = 0; u < G; ++u) {
-        row0[u] = a.route_row ? v[u] : v[u] * a.T + t;
+        // (an out-of-range index is never used: it clears ok)
+        row0[u] = a.route_row ? v[u] : (v[u] >= 0 && v[u] < a.E ? v[u] * a.T + t : 0);
         w0[u] = wv[u];
       }
     }
