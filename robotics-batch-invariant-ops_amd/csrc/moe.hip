@@ -403,14 +403,17 @@ __global__ __launch_bounds__(256) void moe_route_rows_kernel(PackArgs a) {
 // route r; the lanes of one wavefront holding the same bucket find each other by ballots, and
 // bucket b's count per wavefront goes to LDS; thread b then turns the 16 counts into the routes
 // of earlier wavefronts, and a workgroup scan over the buckets places rows and m-tiles.
+// The workgroup has the fewest of 2 / 4 / 8 / 16 wavefronts that give every route and every
+// bucket a thread.
 constexpr int kSmallPackRoutes = 1024;  // routes (one per thread)
 constexpr int kSmallPackBuckets = 512;  // experts + 1 (the bucket of invalid indices)
-constexpr int kSmallPackWaves = kSmallPackRoutes / 64;
 
-__global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackArgs a) {
-  __shared__ int32_t cnt[kSmallPackWaves][kSmallPackBuckets];
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void moe_pack_small_kernel(PackArgs a) {
+  static_assert(WAVES * 64 <= kSmallPackRoutes, "one thread per route");
+  __shared__ int32_t cnt[WAVES][kSmallPackBuckets];
   __shared__ int32_t first_row[kSmallPackBuckets];
-  __shared__ int32_t wsum[kSmallPackWaves][3];
+  __shared__ int32_t wsum[WAVES][3];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int E = (int)a.E, E1 = E + 1;
   for (int b = lane; b < E1; b += 64) cnt[w][b] = 0;
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
   lds_sync();
   int32_t n = 0;  // routes of bucket tid
   if (tid < E1) {
-    for (int v = 0; v < kSmallPackWaves; ++v) {
+    for (int v = 0; v < WAVES; ++v) {
       const int32_t c = cnt[v][tid];
       cnt[v][tid] = n;
       n += c;
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(kSmallPackRoutes) void moe_pack_small_kernel(PackAr
       g[0] = tid; g[1] = row0 + m; g[2] = row0 + n; g[3] = 0;
     }
   }
-  if (tid == kSmallPackRoutes - 1) {
+  if (tid == WAVES * 64 - 1) {
     a.grp1[0] = p1 + i1;
     a.grp2[0] = p2 + i2;
   }
@@ -703,7 +706,11 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
     p.tail1 = small ? 0 : grouped_tail_rows(dtype, g.gu, kEpiSwiglu, g.gu_kmajor);
     p.tail2 = small ? 0 : grouped_tail_rows(dtype, g.dn, kEpiPlain, g.dn_kmajor);
     if (small) {
-      hipLaunchKernelGGL(moe_pack_small_kernel, dim3(1), dim3(kSmallPackRoutes), 0, s, p);
+      const int64_t threads = std::max<int64_t>(R, experts + 1);
+      if (threads <= 128) hipLaunchKernelGGL(moe_pack_small_kernel<2>, dim3(1), dim3(128), 0, s, p);
+      else if (threads <= 256) hipLaunchKernelGGL(moe_pack_small_kernel<4>, dim3(1), dim3(256), 0, s, p);
+      else if (threads <= 512) hipLaunchKernelGGL(moe_pack_small_kernel<8>, dim3(1), dim3(512), 0, s, p);
+      else hipLaunchKernelGGL(moe_pack_small_kernel<16>, dim3(1), dim3(1024), 0, s, p);
       if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
     } else {
       const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);
