@@ -25,8 +25,11 @@ __all__ = [
     "mean_dims",
     "vector_norm",
     "sdpa",
+    "sdpa_abs",
     "varlen_sdpa",
+    "varlen_sdpa_abs",
     "moe",
+    "moe_abs",
     "conv",
     "conv_abs",
     "gemm_abs",
@@ -129,10 +132,9 @@ def _scalar_to_opmath(scale: float) -> float:
     return float(torch.tensor(scale, dtype=torch.float32))
 
 
-def sdpa(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False):
-    """Eager attention with the reference's roundings (BIO 1148-1213):
-    S = round(Q K^T); S = round(S * scale); causal top-left / bool mask -> -inf, additive mask
-    -> round(S + mask); P = softmax(S) in q.dtype; O = round(P V)."""
+def _sdpa_probs(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False):
+    """The probabilities P (rounded to q.dtype, held in float64) and the GQA-expanded V of
+    ``sdpa``; the roundings are listed there."""
     dt = q.dtype
     if enable_gqa:
         rep = q.shape[-3] // k.shape[-3]
@@ -152,17 +154,31 @@ def sdpa(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False)
         else:
             res_dtype = torch.promote_types(dt, attn_mask.dtype)
             s = rnd(s + attn_mask.double(), res_dtype)
-    p = softmax(s, dim=-1, dtype=dt).double()
-    return rnd(p @ v.double(), dt).to(dt)
+    return softmax(s, dim=-1, dtype=dt).double(), v
 
 
-def varlen_sdpa(q, k, v, cu_q, cu_kv, *, is_causal=False, causal_type=None, scale=None):
-    """Packed varlen attention (BIO 1216-1344): each sequence alone; rows outside every
-    sequence and sequences with empty key ranges are zero; BottomRight causal keeps
-    j <= i + (kv - q), TopLeft / None keeps j <= i."""
+def sdpa(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False):
+    """Eager attention with the reference's roundings (BIO 1148-1213):
+    S = round(Q K^T); S = round(S * scale); causal top-left / bool mask -> -inf, additive mask
+    -> round(S + mask); P = softmax(S) in q.dtype; O = round(P V)."""
+    p, v = _sdpa_probs(q, k, v, attn_mask, is_causal, scale, enable_gqa)
+    return rnd(p @ v.double(), q.dtype).to(q.dtype)
+
+
+def sdpa_abs(q, k, v, attn_mask=None, is_causal=False, scale=None, enable_gqa=False):
+    """P |V| in float64 with the P of ``sdpa``: the per-element scale of the output's error
+    bound (one ulp of a probability moves an output by at most that ulp times P |V|)."""
+    p, v = _sdpa_probs(q, k, v, attn_mask, is_causal, scale, enable_gqa)
+    return p @ v.double().abs()
+
+
+def _varlen(q, k, v, cu_q, cu_kv, is_causal, causal_type, scale, per_sequence):
+    """Packed varlen attention (BIO 1216-1344): each sequence alone through ``per_sequence``
+    (``sdpa`` or ``sdpa_abs``); rows outside every sequence and sequences with empty key
+    ranges are zero; BottomRight causal keeps j <= i + (kv - q), TopLeft / None keeps j <= i."""
     cu_q = [int(x) for x in cu_q]
     cu_kv = [int(x) for x in cu_kv]
-    out = torch.zeros((1, q.shape[1], q.shape[2], v.shape[3]), dtype=v.dtype)
+    out = None
     name = getattr(causal_type, "name", None)
     if name is None and causal_type is not None:
         name = str(causal_type).rsplit(".", 1)[-1]
@@ -181,37 +197,67 @@ def varlen_sdpa(q, k, v, cu_q, cu_kv, *, is_causal=False, causal_type=None, scal
             shift = kl - ql if name == "BottomRight" else 0
             mask = ki_idx <= qi_idx + shift
             causal = False
-        o = sdpa(qi, ki, vi, attn_mask=mask, is_causal=causal, scale=scale,
-                 enable_gqa=qi.shape[-3] != ki.shape[-3])
+        o = per_sequence(qi, ki, vi, attn_mask=mask, is_causal=causal, scale=scale,
+                         enable_gqa=qi.shape[-3] != ki.shape[-3])
+        if out is None:
+            out = torch.zeros((1, q.shape[1], q.shape[2], v.shape[3]), dtype=o.dtype)
         out[:, q0:q1] = o.transpose(1, 2)
+    if out is None:
+        out = torch.zeros((1, q.shape[1], q.shape[2], v.shape[3]), dtype=v.dtype)
     return out
 
 
+def varlen_sdpa(q, k, v, cu_q, cu_kv, *, is_causal=False, causal_type=None, scale=None):
+    """Packed varlen attention with the rules of ``_varlen``, in the input dtype."""
+    return _varlen(q, k, v, cu_q, cu_kv, is_causal, causal_type, scale, sdpa).to(v.dtype)
+
+
+def varlen_sdpa_abs(q, k, v, cu_q, cu_kv, *, is_causal=False, causal_type=None, scale=None):
+    """P |V| per packed output element (float64; zero where the output is zero)."""
+    return _varlen(q, k, v, cu_q, cu_kv, is_causal, causal_type, scale, sdpa_abs).double()
+
+
 # ---------------------------------------------------------------------------- MoE ----
-def moe(hidden, routing_weights, selected, gate, up, down):
-    """Dense top-k SwiGLU MoE with the reference's roundings (MOE 75-91):
+def _moe_routes(hidden, routing_weights, selected, gate, up, down):
+    """The weighted routes round(y[sel] * round(w)) of every slot, in slot order (MOE 75-87):
     g = round(x gate_e^T), u = round(x up_e^T), a = round(round(silu(g)) * u),
-    y = round(a down_e^T), route = round(y[sel] * round(w)), out = fixed left-to-right slot sum
-    with a rounding after every add."""
+    y = round(a down_e^T)."""
     dt = hidden.dtype
     x = hidden.double()
     T, k = selected.shape
-    D = hidden.shape[1]
-    if T == 0:
-        return hidden.new_empty((0, D))
-    if k == 0:
-        return hidden.new_zeros((T, D))
     g = rnd(torch.einsum("td,eid->eti", x, gate.double()), dt)
     u = rnd(torch.einsum("td,eid->eti", x, up.double()), dt)
     a = rnd(rnd(g / (1.0 + torch.exp(-g)), dt) * u, dt)
     y = rnd(torch.einsum("eti,edi->etd", a, down.double()), dt)
     w = rnd(routing_weights.double(), dt)
     t_idx = torch.arange(T)
+    return [rnd(y[selected[:, s], t_idx] * w[:, s : s + 1], dt) for s in range(k)]
+
+
+def moe(hidden, routing_weights, selected, gate, up, down):
+    """Dense top-k SwiGLU MoE with the reference's roundings (MOE 75-91): the routes of
+    ``_moe_routes`` summed left to right over the slots with a rounding after every add."""
+    dt = hidden.dtype
+    T, k = selected.shape
+    D = hidden.shape[1]
+    if T == 0:
+        return hidden.new_empty((0, D))
+    if k == 0:
+        return hidden.new_zeros((T, D))
     out = None
-    for s in range(k):
-        route = rnd(y[selected[:, s], t_idx] * w[:, s : s + 1], dt)
+    for route in _moe_routes(hidden, routing_weights, selected, gate, up, down):
         out = route if out is None else rnd(out + route, dt)
     return out.to(dt)
+
+
+def moe_abs(hidden, routing_weights, selected, gate, up, down):
+    """sum over the slots of |round(w) y| (float64): the per-element scale of the output's error
+    bound (one ulp of a route or of a partial sum is at most one ulp of this sum)."""
+    T, k = selected.shape
+    out = torch.zeros(T, hidden.shape[1], dtype=torch.float64)
+    for route in _moe_routes(hidden, routing_weights, selected, gate, up, down) if T and k else ():
+        out = out + route.abs()
+    return out
 
 
 # -------------------------------------------------------------------- convolution ----

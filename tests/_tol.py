@@ -75,3 +75,49 @@ def assert_bitwise(a: torch.Tensor, b: torch.Tensor, what: str = "") -> None:
     ib = b.contiguous().view(torch.int16 if b.element_size() == 2 else torch.int32)
     diff = int((ia != ib).sum())
     assert diff == 0, f"{what}: {diff} elements differ bitwise"
+
+
+# Share of elements that must carry the oracle's exact bits in a composite op's 16-bit output.
+# The kernels round where the oracle rounds, so only elements whose fp32 sums straddle a
+# rounding boundary may differ (fp32 emulations on the CPU: over 99.8 % equal in bf16, over 98 %
+# in fp16).  One dropped intermediate rounding, a reordered slot sum or a wrong GQA head map
+# leaves under 60 % equal (the same emulations), so these shares catch such mistakes where an
+# error bound alone cannot.
+MIN_EXACT = {torch.bfloat16: 0.97, torch.float16: 0.95, torch.float32: 0.0}
+
+
+def assert_composite_close(actual, expected, scale, *, n: int = 2, min_exact: float | None = None,
+                           what: str = ""):
+    """Composite ops (attention, MoE) against the float64 oracle, in two parts.
+
+    * Every element: |a - e| <= r * (|e| + n * scale).  ``scale`` is the oracle's per-element
+      magnitude of the summed terms (P |V| for attention, sum_s |round(w_s) y_s| for MoE); an
+      intermediate that lands one ulp (r) away moves the output by at most r times that
+      magnitude, and the final rounding adds one ulp of the output.  r is the output dtype's ulp
+      (2^-7 bf16, 2^-10 fp16) or the north-star rtol 1e-5 for fp32.
+    * The share of elements bitwise equal to the oracle is at least ``min_exact`` (default
+      ``MIN_EXACT`` by dtype).
+    """
+    dtype = actual.dtype
+    r = 1e-5 if dtype == torch.float32 else ULP[dtype]
+    a = actual.detach().double().cpu()
+    e = expected.detach().double().cpu()
+    s = scale.detach().double().cpu()
+    nan_a, nan_e = torch.isnan(a), torch.isnan(e)
+    assert torch.equal(nan_a, nan_e), f"{what}: NaN pattern differs"
+    a = torch.where(nan_a, torch.zeros_like(a), a)
+    e = torch.where(nan_e, torch.zeros_like(e), e)
+    err = (a - e).abs()
+    bound = r * (e.abs() + n * s)
+    bad = ~(err <= bound)
+    worst = int((err - bound).flatten().argmax()) if err.numel() else 0
+    assert not bool(bad.any()), (
+        f"{what}: {int(bad.sum())} of {bad.numel()} elements outside the per-element bound; worst err "
+        f"{float(err.flatten()[worst]):.3e} at a bound of {float(bound.flatten()[worst]):.3e}"
+    )
+    if min_exact is None:
+        min_exact = MIN_EXACT[dtype]
+    exact = float((a == e).double().mean()) if a.numel() else 1.0
+    print(f"[parity] {what}: {exact:.4f} of {a.numel()} elements bitwise equal", flush=True)
+    assert exact >= min_exact, (
+        f"{what}: only {exact:.4f} of the elements carry the oracle's bits (at least {min_exact} expected)")

@@ -1,9 +1,11 @@
 """Deterministic token-choice MoE on the GPU (reference tests test_batch_invariance.py:745-780).
 
-Parity bound: the MoE rounds gate, up, silu(gate), the SwiGLU product, the down projection, each
-weighted route and each partial slot sum.  Each of those roundings can differ by one ulp when the
-fp32 accumulations straddle a rounding boundary, so the bound is (4 + top_k) ulps of the output
-dtype relative to max|y| over the routes, plus the fp32 accumulation term.
+Parity: the MoE rounds gate, up, silu(gate), the SwiGLU product, the down projection, each
+weighted route and each partial slot sum, where the reference does.  Random inputs are checked
+per element (one ulp of the output dtype times |out| + (2 + top_k) times the token's sum of
+route magnitudes) and by the share of elements carrying the oracle's exact bits
+(tests/_parity.py); the known-answer cases (tests/_moe_known.py) pin each rounding and the slot
+order exactly, on the dense and the sparse evaluation and on every token alone.
 """
 
 import pytest
@@ -13,6 +15,10 @@ import torch.nn.functional as F
 import oracle
 from batch_invariant_ops import deterministic_token_choice_moe as moe
 
+from batch_invariant_ops.moe import _moe
+
+from _moe_known import CASES, known_answer_problem, midpoint_margin, silu_sweep_problem
+from _parity import check_moe
 from _tol import ULP, assert_bitwise, assert_close_scaled
 
 pytestmark = pytest.mark.gpu
@@ -61,10 +67,7 @@ def test_moe_matches_oracle(dtype):
     down = randn(E, D, I, seed=7413, dtype=dtype, scale=0.2)
     w, sel = routing(T, E, k, 7414)
     out = moe(*(t.cuda() for t in (hidden, w, sel, gate, up, down)))
-    ref = oracle.moe(hidden, w, sel, gate, up, down)
-    scale = float(ref.double().abs().max())
-    n = 4 + k
-    assert_close_scaled(out, ref, rel=n * ULP[dtype], abs_scale=n * ULP[dtype] * scale, what="moe")
+    check_moe(out, hidden, w, sel, gate, up, down, what=f"moe {dtype}")
 
 
 def test_moe_is_batch_invariant():
@@ -91,12 +94,10 @@ def test_moe_fused_gate_up_layout():
     w, sel = routing(T, E, k, 7443)
     gate, up, down = gu[..., :I].transpose(1, 2), gu[..., I:].transpose(1, 2), dn.transpose(1, 2)
     out = moe(hidden.cuda(), w.cuda(), sel.cuda(), gate.cuda(), up.cuda(), down.cuda())
-    ref = oracle.moe(hidden, w, sel, gate, up, down)
     contiguous = moe(hidden.cuda(), w.cuda(), sel.cuda(), gate.contiguous().cuda(), up.contiguous().cuda(),
                      down.contiguous().cuda())
     assert_bitwise(out, contiguous, "strided vs contiguous weights")
-    scale = float(ref.double().abs().max())
-    assert_close_scaled(out, ref, rel=6 * ULP[torch.bfloat16], abs_scale=6 * ULP[torch.bfloat16] * scale)
+    check_moe(out, hidden, w, sel, gate, up, down, what="fused gate_up layout")
 
 
 def test_moe_edge_cases(monkeypatch):
@@ -120,3 +121,42 @@ def test_moe_edge_cases(monkeypatch):
     monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "1")
     with pytest.raises(RuntimeError, match="outside"):
         moe(hidden, torch.ones(3, 1, device="cuda"), bad_sel, gate, gate, down)
+
+
+@pytest.mark.parametrize("sparse", (False, True), ids=("dense", "sparse"))
+def test_moe_known_answers(sparse):
+    """Each token is one case of tests/_moe_known.py: the silu rounding, the silu*up rounding,
+    the routing weight's rounding, the weighted route's rounding and the left-to-right slot sum
+    each decide its output bits.  Checked exactly, for the whole batch and for every token alone
+    (the few-token calls run other GEMM tile entries and the one-workgroup route packing)."""
+    hidden, weights, selected, gate, up, down, expected = known_answer_problem()
+    args = [t.cuda() for t in (hidden, weights, selected, gate, up, down)]
+    out = _moe(*args, sparse=sparse)
+    for t, (name, _, value, mistake) in enumerate(CASES):
+        got = out[t, 0].item()
+        assert got == value, f"token {t} ({name}): {got}, expected {value} ({mistake} would be the mistake)"
+    assert_bitwise(out, expected.cuda(), "known answers")
+    for t in range(len(CASES)):
+        alone = _moe(*(a[t : t + 1] for a in args[:3]), *args[3:], sparse=sparse)
+        assert_bitwise(alone, expected[t : t + 1].cuda(), f"token {t} alone ({CASES[t][0]})")
+
+
+@pytest.mark.parametrize("u", (1.5, -1.75))
+def test_moe_swiglu_epilogue_over_every_bf16_gate_value(u):
+    """round(round(silu(g)) * u) for every bf16 g with 2^-4 <= |g| < 8 (1792 tokens): the dense
+    and the sparse evaluation both give the oracle's bits, except where silu(g) lies within
+    10^-5 of its magnitude of a bf16 rounding midpoint (an fp32 silu may land on either side;
+    there one ulp is allowed)."""
+    problem, g = silu_sweep_problem(u)
+    ref = oracle.moe(*problem)[:, 0].double()
+    silu = g.double() / (1 + torch.exp(-g.double()))
+    tight = midpoint_margin(silu) < 1e-5
+    args = [t.cuda() for t in problem]
+    for sparse in (False, True):
+        got = _moe(*args, sparse=sparse)[:, 0].cpu().double()
+        assert torch.count_nonzero(_moe(*args, sparse=sparse)[:, 1:]) == 0
+        exact = got == ref
+        assert bool(exact[~tight].all()), (
+            f"sparse={sparse}: {int((~exact[~tight]).sum())} of {int((~tight).sum())} tokens differ, first at "
+            f"g = {float(g[~tight][~exact[~tight]][0])}")
+        assert bool(((got - ref).abs() <= ULP[torch.bfloat16] * ref.abs())[tight].all())

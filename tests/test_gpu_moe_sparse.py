@@ -17,6 +17,7 @@ import oracle
 from batch_invariant_ops import _native as nat
 from batch_invariant_ops.moe import _moe
 
+from _parity import check_moe
 from _tol import ULP, assert_bitwise, assert_close_scaled
 
 pytestmark = pytest.mark.gpu
@@ -62,11 +63,7 @@ def test_sparse_matches_oracle_bf16():
     sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
     w = torch.rand(T, k, generator=g)
     out = _moe(*(t.cuda() for t in (hidden, w, sel, gate, up, down)), sparse=True)
-    ref = oracle.moe(hidden, w, sel, gate, up, down)
-    scale = float(ref.double().abs().max())
-    n = 4 + k
-    dt = torch.bfloat16
-    assert_close_scaled(out, ref, rel=n * ULP[dt], abs_scale=n * ULP[dt] * scale, what="sparse moe")
+    check_moe(out, hidden, w, sel, gate, up, down, what="sparse moe")
 
 
 def test_sparse_skewed_routing():

@@ -22,6 +22,7 @@ from batch_invariant_ops import (
     softmax,
 )
 
+from _parity import check_sdpa
 from _tol import ULP, assert_bitwise, assert_close_scaled, assert_gemm_close
 
 pytestmark = pytest.mark.gpu
@@ -114,6 +115,5 @@ def test_random_sdpa(case):
     j = rng.randrange(b)
     alone = sdpa(q[j : j + 1].cuda(), k[j : j + 1].cuda(), v[j : j + 1].cuda(), **kw)
     assert_bitwise(alone, out[j : j + 1], f"sample {j} of {b} ({hq}/{hkv} heads, {lq}x{lk}, d {d}/{dv}, {dtype})")
-    vmax = max(float(v.double().abs().max()), 1.0)
-    assert_close_scaled(out, oracle.sdpa(q, k, v, **kw), rel=4 * ULP[dtype], abs_scale=4 * ULP[dtype] * vmax,
-                        what="sdpa")
+    # few elements per case: the share of exact bits is left to the larger tests
+    check_sdpa(out, q, k, v, min_exact=0.0 if out.numel() < 4096 else None, what=f"sdpa case {case}", **kw)

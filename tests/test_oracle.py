@@ -214,6 +214,29 @@ def test_sdpa_rounds_each_bf16_intermediate(case):
     assert 0.6 < unrounded.item() < 0.75
 
 
+def test_sdpa_abs_closed_forms():
+    """P |V|: uniform attention gives the mean of |V| (the prefix means under causal); a
+    one-hot attention row (one key far above the others) gives that key's |V| row."""
+    g = torch.Generator().manual_seed(12)
+    q = torch.zeros(1, 1, 4, 8)
+    k = torch.randn(1, 1, 4, 8, generator=g)
+    v = torch.randn(1, 1, 4, 3, generator=g)
+    assert torch.allclose(oracle.sdpa_abs(q, k, v), v.abs().double().mean(-2, keepdim=True).expand(1, 1, 4, 3))
+    prefix = torch.cumsum(v.abs().double(), -2) / torch.arange(1, 5).reshape(1, 1, 4, 1)
+    assert torch.allclose(oracle.sdpa_abs(q, k, v, is_causal=True), prefix)
+    q1 = torch.tensor([[[[100.0, 0.0]]]])
+    k1 = torch.tensor([[[[1.0, 0.0], [-1.0, 0.0], [0.0, 0.0]]]])
+    v1 = torch.tensor([[[[-2.0, 3.0], [5.0, 7.0], [1.0, 1.0]]]])
+    assert oracle.sdpa_abs(q1, k1, v1, scale=1.0)[0, 0, 0].tolist() == [2.0, 3.0]
+    # varlen: per sequence, zero outside every sequence
+    vv = torch.arange(6, dtype=torch.float32).reshape(1, 6, 1, 1) - 2.5
+    qq, kk = torch.zeros(1, 6, 1, 2), torch.zeros(1, 6, 1, 2)
+    cu = torch.tensor([0, 2, 5])
+    out = oracle.varlen_sdpa_abs(qq, kk, vv, cu, cu)
+    # sequence 0: mean |-2.5|, |-1.5|; sequence 1: mean of 0.5, 0.5, 1.5 (P = 1/3 in fp32)
+    assert out[0, :, 0, 0].tolist() == pytest.approx([2.0, 2.0, 5 / 6, 5 / 6, 5 / 6, 0.0], rel=1e-7)
+
+
 def test_varlen_alignment_rules_and_zero_rows():
     # two sequences: (q 2, kv 4) and (q 3, kv 3); Q = 0 -> outputs are means of visible V rows
     q = torch.zeros(1, 6, 1, 4)
@@ -268,6 +291,54 @@ def test_moe_slot_sum_is_left_to_right_with_rounding():
     assert oracle.moe(hidden, w, sel, gate, up, down).item() == 1.0
     w2 = torch.tensor([[r, r, 1.0]])
     assert oracle.moe(hidden, w2, sel, gate, up, down).item() == 1 + 2.0**-7
+
+
+def _bf16_scalar(x):
+    return torch.tensor(x, dtype=torch.float64).to(BF16).item()
+
+
+def _known_case_scalar(slots, drop=None):
+    """One known-answer case in Python scalars, each rounding explicit (moe.py:75-91); ``drop``
+    removes one of them or reverses the slot order."""
+    rb = _bf16_scalar
+    routes = []
+    for g, u, c, w in slots:
+        s = g / (1.0 + math.exp(-g))
+        s = s if drop == "silu rounding" else rb(s)
+        a = s * u if drop == "silu*up rounding" else rb(s * u)
+        y = rb(a * c)
+        w = w if drop == "routing weight rounding" else rb(w)
+        routes.append(y * w if drop == "weighted route rounding" else rb(y * w))
+    if drop == "slot order":
+        routes = routes[::-1]
+    out = routes[0]
+    for r in routes[1:]:
+        out = rb(out + r)
+    return rb(out)
+
+
+def test_moe_known_answers():
+    """Each case isolates one rounding of the reference's route evaluation or its slot order:
+    the oracle gives the expected bits, and the named mistake gives the other value."""
+    from _moe_known import CASES, known_answer_problem
+
+    hidden, weights, selected, gate, up, down, expected = known_answer_problem()
+    out = oracle.moe(hidden, weights, selected, gate, up, down)
+    assert torch.equal(out, expected)
+    for name, slots, value, mistake in CASES:
+        assert _known_case_scalar(slots) == value, name
+        assert _known_case_scalar(slots, drop=name) == mistake != value, name
+
+
+def test_moe_abs_is_the_sum_of_route_magnitudes():
+    from _moe_known import CASES, known_answer_problem
+
+    args = known_answer_problem()[:6]
+    scale = oracle.moe_abs(*args)
+    for t, (_, slots, _, _) in enumerate(CASES):
+        mags = [abs(_known_case_scalar([slot])) for slot in slots]
+        assert scale[t, 0].item() == pytest.approx(sum(mags), rel=0, abs=0)
+        assert torch.count_nonzero(scale[t, 1:]) == 0
 
 
 def test_moe_edge_shapes():
