@@ -298,7 +298,8 @@ int64_t biops_moe_workspace_size(int dtype, int64_t tokens, int64_t experts, int
  * its I (resp. D) stride equal to 1.  weights[T,k] in any float dtype w_dtype (each weight is
  * rounded to dtype before the multiply, round(w[t,s]) above), sel[T,k] int64.
  * Expert indices outside [0,E) make the call write zeros for that token and set *bad_index
- * (device int32, may be NULL) to 1.  out[T,D] contiguous.
+ * (device int32, may be NULL) to 1; the flag is never cleared by the library, so one word can
+ * collect the reports of many calls until the caller reads and clears it.  out[T,D] contiguous.
  * Replaces deterministic_token_choice_moe (moe.py:11-92). */
 int biops_moe(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,
               int64_t top_k,
@@ -343,9 +344,11 @@ int biops_moe_sparse(int dtype, int64_t tokens, int64_t experts, int64_t hidden,
  * device current).  Sizes whose biops_moe_sparse_workspace_size exceeds the array return
  * BIOPS_ERR_SIZE before any GPU work (C5 shapes -- hidden 2048, intermediate 768, top-8 -- fit up
  * to 1485 tokens).  The stream must belong to the current device.  Every call on one GPU uses
- * the same array: calls that overlap on one GPU (two streams, or two host threads) race and must
- * be serialised by the caller.  Nothing in the array needs to start at zero: each call writes
- * every table before reading it.
+ * the same array, so the calls on one GPU are ordered on the device: each call's stream waits
+ * for an event recorded after the previous call's kernels (whatever stream or host thread made
+ * it; no host wait).  Under stream capture that wait and record are left out: captured calls
+ * and graph replays that overlap other calls on the same GPU must be ordered by the caller.
+ * Nothing in the array needs to start at zero: each call writes every table before reading it.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid allocation). */
 int biops_moe_sparse_noalloc(int dtype, int64_t tokens, int64_t experts, int64_t hidden, int64_t inter,

@@ -211,6 +211,17 @@ def fast_copy_h2d():
     return _biops_fast.copy_h2d
 
 
+def fast_copy_d2h():
+    """``copy_d2h(dst, src, bytes, stream)`` (hipMemcpyAsync device to host) from the fast-call
+    module, or None when the module is not built."""
+    load()
+    try:
+        from . import _biops_fast
+    except ImportError:
+        return None
+    return _biops_fast.copy_d2h
+
+
 def last_error() -> str:
     """The library's message for the calling thread's last failed call."""
     return load(require_gpu=False).biops_last_error().decode(errors="replace")

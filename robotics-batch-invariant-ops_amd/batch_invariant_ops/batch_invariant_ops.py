@@ -659,10 +659,14 @@ def _offsets_on_host(cu_q, cu_kv):
 
 
 class _VarlenStaging:
-    """The varlen work list's pinned host buffer and device buffer, one pair per (device,
-    stream), reused across calls.  The event recorded after each upload keeps the host buffer
-    untouched until that copy has run; a lock covers the write, the upload and the launch."""
+    """Pinned host buffer + device buffer pairs for the varlen work list, a ring of up to
+    ``RING`` pairs per (device, stream), reused across calls.  The event recorded after each
+    call's upload keeps a pair's host buffer untouched until that copy has run: a call takes
+    the least recently used pair whose event has completed, and waits on an event only when
+    every pair of the ring is still in flight.  A lock covers the choice, the write, the
+    upload and the launch."""
 
+    RING = 4
     _cache: dict = {}
     _lock = threading.Lock()
     _h2d = None  # the fast-call module's host-to-device copy, False without the module
@@ -675,15 +679,25 @@ class _VarlenStaging:
 
     @classmethod
     def get(cls, device, stream, words):
-        key = (device.index, stream)
-        st = cls._cache.get(key)
-        if st is not None:
-            st.event.synchronize()  # the last upload from the host buffer has run
-        if st is None or st.view.size < words:
+        ring = cls._cache.setdefault((device.index, stream), [])  # least recently used first
+        idle = None
+        for i, st in enumerate(ring):
+            if st.event.query():  # the last upload from this host buffer has run
+                if st.view.size >= words:
+                    ring.append(ring.pop(i))
+                    return st
+                idle = i if idle is None else idle
+        if len(ring) < cls.RING:
+            ring.append(cls(max(words, 4096), device))
+            return ring[-1]
+        i = 0 if idle is None else idle
+        ring[i].event.synchronize()
+        if ring[i].view.size < words:
             # a grown pair replaces the old one (the device buffer goes back to torch's stream-
             # ordered allocator; the work queued on it runs first)
-            st = cls._cache[key] = cls(max(words, 4096, 2 * (st.view.size if st else 0)), device)
-        return st
+            ring[i] = cls(max(words, 2 * ring[i].view.size), device)
+        ring.append(ring.pop(i))
+        return ring[-1]
 
     def upload(self, used, stream):
         """The first ``used`` words of the host buffer to the device buffer, on ``stream``,

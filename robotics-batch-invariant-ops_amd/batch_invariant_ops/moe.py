@@ -2,9 +2,93 @@
 
 from __future__ import annotations
 
+import threading
+import time
+
 import torch
 
 from . import _native as nat
+
+_INDEX_ERROR = "selected_experts contains an expert index outside [0, num_experts)"
+
+
+class _IndexWatch:
+    """Deferred report of out-of-range expert indices on one device, without a host wait.
+
+    Every MoE call passes the device's flag word to the kernels, which set it to 1 when a
+    token selects an expert outside [0, E) (and write that token's row as zeros); they never
+    clear it.  At most one asynchronous copy of the flag into a pinned host word is in flight,
+    started after a call when the last one has landed and ``PERIOD`` seconds have passed (none
+    during stream capture).  The next call, or ``check_moe_indices``, reads a landed copy and
+    raises ``RuntimeError`` if the flag was set, after clearing it."""
+
+    PERIOD = 1e-3
+    _by_device: dict = {}
+    _lock = threading.Lock()
+
+    def __init__(self, device: torch.device):
+        self.flag = torch.zeros(1, dtype=torch.int32, device=device)
+        self.host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.pending = False
+        self.last = 0.0
+        self.copy = nat.fast_copy_d2h()
+
+    @classmethod
+    def of(cls, device: torch.device) -> "_IndexWatch":
+        watch = cls._by_device.get(device.index)
+        if watch is None:
+            with cls._lock:
+                watch = cls._by_device.setdefault(device.index, cls(device))
+        return watch
+
+    def _raise_if_set(self, value: int) -> None:
+        if value != 0:
+            self.host[0] = 0
+            self.flag.zero_()
+            raise RuntimeError(f"{_INDEX_ERROR} in a call since the last report")
+
+    def poll(self) -> None:
+        """Raise for a flag copy that has landed with the flag set."""
+        if self.pending and self.event.query():
+            self.pending = False
+            self._raise_if_set(int(self.host[0]))
+
+    def after_call(self, stream: int) -> None:
+        """Start a flag copy on ``stream`` unless one is in flight, one started less than
+        PERIOD seconds ago, or the stream is being captured."""
+        if self.pending:
+            return
+        now = time.monotonic()
+        if now - self.last < self.PERIOD or torch.cuda.is_current_stream_capturing():
+            return
+        self.last = now
+        if self.copy is not None:
+            rc = self.copy(self.host.data_ptr(), self.flag.data_ptr(), 4, stream)
+            if rc != 0:
+                raise RuntimeError(f"hipMemcpyAsync of the MoE index flag failed ({rc})")
+        else:
+            self.host.copy_(self.flag, non_blocking=True)
+        self.event.record()
+        self.pending = True
+
+    def check(self) -> None:
+        """Wait for the work queued so far on the current stream and raise if any of it (or an
+        earlier call) saw an out-of-range index."""
+        self.pending = False
+        self._raise_if_set(int(self.flag.item()))
+
+
+def check_moe_indices(device: torch.device | int | None = None) -> None:
+    """Raise ``RuntimeError`` if a ``deterministic_token_choice_moe`` call on ``device``
+    (default: the current device) met an expert index outside [0, num_experts) since the last
+    report.  Waits for the work queued on that device's current stream."""
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    elif isinstance(device, int):
+        device = torch.device("cuda", device)
+    with torch.cuda.device(device):
+        _IndexWatch.of(device).check()
 
 
 def _unit_stride_weight(w: torch.Tensor) -> torch.Tensor:
@@ -38,11 +122,12 @@ def deterministic_token_choice_moe(
     selects (also used above 2048 experts).
 
     Expert indices outside ``[0, E)`` never make a kernel read out of range: the token's output
-    row is written as zeros.  The call does not wait for the GPU to report them (a host read
-    would synchronise every call, and would fail under stream capture).  With
-    ``BIOPS_MOE_CHECK_INDICES=1`` the call waits for the kernels and raises ``RuntimeError``
-    when an index was out of range.  The reference asserts on the device instead
-    (moe.py:66-73), which ends the process's GPU context.
+    row is written as zeros, and the error is reported without a host wait in the call.  The
+    kernels set a device flag, an asynchronous copy brings it to the host, and a later call
+    (or ``check_moe_indices()``, which waits) raises ``RuntimeError`` once the copy has landed.
+    With ``BIOPS_MOE_CHECK_INDICES=1`` each call waits for its kernels and raises at once.  The
+    reference asserts on the device instead (moe.py:66-73), which ends the process's GPU
+    context.
     """
     del workspace
     return _moe(hidden_states, routing_weights, selected_experts, gate_weight, up_weight, down_weight,
@@ -109,8 +194,10 @@ def _moe(
         ws_bytes = lib.biops_moe_workspace_size(code, token_count, num_experts, hidden_size, intermediate_size)
     # torch's caching allocator returns 512-byte aligned blocks (the sparse path needs 256).
     scratch = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=x.device)
+    watch = _IndexWatch.of(x.device)
+    watch.poll()
     check = nat.env_flag("BIOPS_MOE_CHECK_INDICES", False)
-    bad = torch.zeros(1, dtype=torch.int32, device=x.device) if check else None
+    stream = nat.stream_of(out)
     nat.call(
         entry,
         code, token_count, num_experts, hidden_size, intermediate_size, top_k,
@@ -119,10 +206,12 @@ def _moe(
         up.data_ptr(), *up.stride(),
         down.data_ptr(), *down.stride(),
         weights.data_ptr(), w_code, selected.data_ptr(),
-        out.data_ptr(), bad.data_ptr() if check else None,
+        out.data_ptr(), watch.flag.data_ptr(),
         scratch.data_ptr(), scratch.numel(),
-        nat.stream_of(out),
+        stream,
     )
-    if check and int(bad.item()) != 0:
-        raise RuntimeError("selected_experts contains an expert index outside [0, num_experts)")
+    if check:
+        watch.check()
+    else:
+        watch.after_call(stream)
     return out

@@ -53,12 +53,24 @@ def _compile(src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
+def _stale(src: pathlib.Path) -> bool:
+    """The object of ``src`` is missing or older than ``src`` or any csrc / include header."""
+    obj = BUILD / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.h"), *(ROOT.parent / "include").glob("*.h")]
+    return obj.stat().st_mtime < max(d.stat().st_mtime for d in deps)
+
+
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> pathlib.Path:
+    """Compile every source (``incremental``: only those whose object is stale) and link."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
+    todo = [s for s in sources if _stale(s)] if incremental else sources
+    jobs = jobs or min(max(len(todo), 1), max(1, (os.cpu_count() or 2)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(_compile, sources))
+        list(pool.map(_compile, todo))
+    objects = [BUILD / (s.stem + ".o") for s in sources]
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -92,5 +104,7 @@ def _build_fast() -> pathlib.Path:
 if __name__ == "__main__":
     parser = argparse.ArgumentParser()
     parser.add_argument("--jobs", type=int, default=None)
+    parser.add_argument("--incremental", action="store_true",
+                        help="recompile only sources whose object is older than the source or a header")
     args = parser.parse_args()
-    build(args.jobs)
+    build(args.jobs, incremental=args.incremental)

@@ -748,6 +748,17 @@ namespace {
 constexpr int kMaxScratchDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
 std::mutex g_scratch_mutex;
+
+// Order of the calls that share a device's array: each call's stream waits (on the device, not
+// the host) for an event recorded after the previous call's last kernel, whatever stream that
+// call used.  The mutex orders the host side: the wait, the launches and the record of one
+// call are not interleaved with another thread's.
+struct ScratchOrder {
+  std::mutex m;
+  hipEvent_t done = nullptr;  // created on the device's first call
+  bool recorded = false;
+};
+ScratchOrder g_scratch_order[kMaxScratchDevices];
 }  // namespace
 
 // Device address of `scratch` on the current device, looked up once per device (with that
@@ -807,7 +818,36 @@ extern "C" int biops_moe_sparse_noalloc(int dtype, int64_t tokens, int64_t exper
   if (tokens == 0 || hidden == 0) return BIOPS_OK;
   void* ws = nullptr;
   if ((rc = noalloc_scratch(&ws)) != BIOPS_OK) return rc;
-  return moe_sparse_run(dtype, tokens, experts, hidden, inter, top_k, x, sx, gate, sgE, sgI, sgD, up, suE,
-                        suI, suD, down, sdE, sdD, sdI, weights, w_dtype, sel, out, bad_index, ws,
-                        BIOPS_MOE_NOALLOC_SCRATCH_BYTES, stream);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(BIOPS_ERR_HIP, "no current HIP device");
+  hipStream_t s = (hipStream_t)stream;
+  // Under stream capture the wait and the record are left out: a captured stream cannot wait on
+  // an event recorded outside the capture, and a graph's replays on one stream run in order.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &capture) != hipSuccess)
+    return fail(BIOPS_ERR_HIP, "hipStreamIsCapturing failed");
+  const bool order = capture == hipStreamCaptureStatusNone;
+  ScratchOrder& o = g_scratch_order[dev];
+  std::lock_guard<std::mutex> lock(o.m);
+  if (order) {
+    if (o.done == nullptr) {
+      const hipError_t e = hipEventCreateWithFlags(&o.done, hipEventDisableTiming);
+      if (e != hipSuccess) return fail(BIOPS_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
+    }
+    if (o.recorded) {
+      const hipError_t e = hipStreamWaitEvent(s, o.done, 0);
+      if (e != hipSuccess) return fail(BIOPS_ERR_HIP, "hipStreamWaitEvent: %s", hipGetErrorString(e));
+    }
+  }
+  rc = moe_sparse_run(dtype, tokens, experts, hidden, inter, top_k, x, sx, gate, sgE, sgI, sgD, up, suE, suI,
+                      suD, down, sdE, sdD, sdI, weights, w_dtype, sel, out, bad_index, ws,
+                      BIOPS_MOE_NOALLOC_SCRATCH_BYTES, s);
+  if (order) {
+    // recorded even after a failed launch, so that a later call never waits on work that
+    // was not queued
+    const hipError_t e = hipEventRecord(o.done, s);
+    if (e != hipSuccess && rc == BIOPS_OK) return fail(BIOPS_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(e));
+    o.recorded = o.recorded || e == hipSuccess;
+  }
+  return rc;
 }

@@ -15,7 +15,7 @@ import torch.nn.functional as F
 import oracle
 from batch_invariant_ops import deterministic_token_choice_moe as moe
 
-from batch_invariant_ops.moe import _moe
+from batch_invariant_ops.moe import _IndexWatch, _moe, check_moe_indices
 
 from _moe_known import CASES, known_answer_problem, midpoint_margin, silu_sweep_problem
 from _parity import check_moe
@@ -121,6 +121,38 @@ def test_moe_edge_cases(monkeypatch):
     monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "1")
     with pytest.raises(RuntimeError, match="outside"):
         moe(hidden, torch.ones(3, 1, device="cuda"), bad_sel, gate, gate, down)
+    check_moe_indices()  # the report above cleared the flag
+
+
+@pytest.mark.parametrize("sparse", (False, True), ids=("dense", "sparse"))
+def test_moe_reports_out_of_range_indices_without_waiting(monkeypatch, sparse):
+    """The reference rejects out-of-range expert indices (moe.py:66-73).  Here the call itself
+    does not wait: the kernels set a device flag, an asynchronous copy brings it to the host,
+    and the next call after the copy has landed raises RuntimeError (so does
+    check_moe_indices(), which waits).  One report clears the flag."""
+    monkeypatch.delenv("BIOPS_MOE_CHECK_INDICES", raising=False)
+    monkeypatch.setattr(_IndexWatch, "PERIOD", 0.0)
+    hidden = randn(4, 16, seed=7460).cuda()
+    gate = randn(3, 8, 16, seed=7461).cuda()
+    down = randn(3, 16, 8, seed=7462).cuda()
+    w = torch.ones(4, 2, device="cuda")
+    good = torch.tensor([[0, 1], [2, 0], [1, 2], [0, 2]], device="cuda")
+    bad = good.clone()
+    bad[2, 1] = 3
+    ref = _moe(hidden, w, good, gate, gate, down, sparse=sparse)
+    check_moe_indices()
+    out = _moe(hidden, w, bad, gate, gate, down, sparse=sparse)  # returns without raising
+    assert torch.count_nonzero(out[2]) == 0
+    assert_bitwise(out[[0, 1, 3]], ref[[0, 1, 3]], "valid tokens of the bad call")
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="outside"):
+        _moe(hidden, w, good, gate, gate, down, sparse=sparse)
+    assert_bitwise(_moe(hidden, w, good, gate, gate, down, sparse=sparse), ref, "after the report")
+    check_moe_indices()
+    _moe(hidden, w, bad, gate, gate, down, sparse=sparse)
+    with pytest.raises(RuntimeError, match="outside"):
+        check_moe_indices()
+    check_moe_indices()
 
 
 @pytest.mark.parametrize("sparse", (False, True), ids=("dense", "sparse"))

@@ -15,7 +15,7 @@ import torch
 
 import oracle
 from batch_invariant_ops import _native as nat
-from batch_invariant_ops.moe import _moe
+from batch_invariant_ops.moe import _IndexWatch, _moe, check_moe_indices
 
 from _parity import check_moe
 from _tol import ULP, assert_bitwise, assert_close_scaled
@@ -33,6 +33,14 @@ def weights_for(E, I, D, seed, dtype, scale=0.1):
     up = randn(E, I, D, seed=seed + 1, dtype=dtype, scale=scale)
     down = randn(E, D, I, seed=seed + 2, dtype=dtype, scale=scale)
     return gate.cuda(), up.cuda(), down.cuda()
+
+
+@pytest.fixture
+def quiet_index_watch(monkeypatch):
+    """Out-of-range indices on purpose: no deferred report between the calls of one test (the
+    test reads the flag itself at the end, with check_moe_indices)."""
+    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
+    monkeypatch.setattr(_IndexWatch, "PERIOD", float("inf"))
 
 
 def both(hidden, w, sel, gate, up, down):
@@ -83,9 +91,8 @@ def test_sparse_skewed_routing():
     assert_bitwise(sparse, dense, "half on expert 0")
 
 
-def test_sparse_invalid_indices(monkeypatch):
+def test_sparse_invalid_indices(quiet_index_watch, monkeypatch):
     """Out-of-range indices: those tokens give zeros on both paths, the others are computed."""
-    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
     T, E, D, I, k = 20, 5, 32, 32, 3
     hidden = randn(T, D, seed=7650, dtype=torch.bfloat16).cuda()
     gate, up, down = weights_for(E, I, D, 7651, torch.bfloat16)
@@ -99,6 +106,8 @@ def test_sparse_invalid_indices(monkeypatch):
     dense, sparse = both(hidden, w, sel, gate, up, down)
     assert_bitwise(sparse, dense, "invalid indices")
     assert torch.count_nonzero(sparse[[3, 7, 19]]) == 0
+    with pytest.raises(RuntimeError, match="outside"):
+        check_moe_indices()
     assert torch.count_nonzero(sparse[0]) > 0
     monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "1")
     with pytest.raises(RuntimeError, match="outside"):
@@ -210,11 +219,10 @@ def test_stream_entries_equal_dense(dtype, T, E, D, I, k):
 
 
 @pytest.mark.parametrize("T,E,k", [(1, 64, 8), (128, 64, 8), (129, 64, 8), (4096, 64, 8), (3, 511, 4), (3, 512, 4)])
-def test_one_workgroup_packing_limits(monkeypatch, T, E, k):
+def test_one_workgroup_packing_limits(quiet_index_watch, T, E, k):
     """Up to 1024 routes and 511 experts the routes are packed by one workgroup, beyond by the
     rank / plan / route-row kernels: both sides of each limit give the dense path's bits,
     with an out-of-range index among the routes."""
-    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
     D, I = 64, 64
     hidden = randn(T, D, seed=7740 + T, dtype=torch.bfloat16).cuda()
     gate, up, down = nmajor_weights(E, I, D, 7741, torch.bfloat16)
@@ -228,6 +236,10 @@ def test_one_workgroup_packing_limits(monkeypatch, T, E, k):
     assert_bitwise(sparse, dense, f"T={T} E={E}")
     if T > 1:
         assert torch.count_nonzero(sparse[T - 1]) == 0
+        with pytest.raises(RuntimeError, match="outside"):
+            check_moe_indices()
+    else:
+        check_moe_indices()
     assert torch.count_nonzero(sparse[0]) > 0
 
 
@@ -254,11 +266,10 @@ def test_tail_m_tiles_equal_dense(cfg):
     assert_bitwise(sparse, dense, f"tile entry {cfg}")
 
 
-def test_plan_over_512_chunks(monkeypatch):
+def test_plan_over_512_chunks(quiet_index_watch):
     """Over 131072 routes (more than 512 chunks of 256) the plan kernel scans each expert's
     chunk counts in several passes; the sparse path still gives the dense path's bits, with
     out-of-range indices among the routes."""
-    monkeypatch.setenv("BIOPS_MOE_CHECK_INDICES", "0")
     T, E, D, I, k = 70000, 5, 64, 64, 2
     hidden = randn(T, D, seed=7770, dtype=torch.bfloat16).cuda()
     gate, up, down = nmajor_weights(E, I, D, 7771, torch.bfloat16)
@@ -271,3 +282,5 @@ def test_plan_over_512_chunks(monkeypatch):
     dense, sparse = both(hidden, w, sel, gate, up, down)
     assert_bitwise(sparse, dense, "140000 routes")
     assert torch.count_nonzero(sparse[12345]) == 0 and torch.count_nonzero(sparse[T - 1]) == 0
+    with pytest.raises(RuntimeError, match="outside"):
+        check_moe_indices()

@@ -95,3 +95,42 @@ def test_noalloc_rejects_sizes_beyond_its_array():
     hidden, weights, selected = _tokens(3, 32, 4, 2, seed=9401)
     assert_bitwise(_noalloc(hidden, weights, selected, gate, up, down),
                    _moe(hidden, weights, selected, gate, up, down, sparse=True), "after a rejected call")
+
+
+def test_noalloc_captured_in_a_graph_replays_new_routing():
+    """The entry's callers include code under stream capture: one call captured in a HIP graph
+    (through torch.cuda.graph) with preallocated inputs and output, replayed three times with
+    new hidden states and routing written into the captured inputs, eager work and a
+    synchronisation between the replays; every replay gives biops_moe_sparse's bits (the array's
+    tables are all rewritten by each replay)."""
+    E, D, I, k, T = 16, 256, 128, 4, 200
+    gate, up, down = _experts(E, D, I, seed=9500)
+    hidden, weights, selected = _tokens(T, D, E, k, seed=9501)
+    x = hidden.clone()
+    w = weights.to(BF16).contiguous()
+    sel = selected.to(torch.int64).contiguous()
+    out = torch.empty(T, D, dtype=BF16, device="cuda")
+    lib = nat.load()
+
+    def call():
+        return lib.biops_moe_sparse_noalloc(
+            nat.BF16, T, E, D, I, k, x.data_ptr(), x.stride(0),
+            gate.data_ptr(), *gate.stride(), up.data_ptr(), *up.stride(), down.data_ptr(), *down.stride(),
+            w.data_ptr(), nat.BF16, sel.data_ptr(), out.data_ptr(), None, nat.stream_of(out))
+
+    nat.check(call(), "eager warm-up")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = call()
+    nat.check(rc, "captured call")
+    for rep in range(3):
+        h2, w2, s2 = _tokens(T, D, E, k, seed=9510 + rep)
+        x.copy_(h2)
+        w.copy_(w2.to(BF16))
+        sel.copy_(s2)
+        print(f"[no-alloc] graph replay {rep}", flush=True)
+        graph.replay()
+        want = _moe(h2, w2.to(BF16), s2, gate, up, down, sparse=True)  # eager work between replays
+        torch.cuda.synchronize()
+        assert_bitwise(out, want, f"replay {rep}")
