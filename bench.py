@@ -9,9 +9,13 @@ linears through the library (linear_batch_invariant -> biops_gemm), inputs resid
 value = sum of FLOPs / wall time of the step.  The line also carries the roofline of the
 dominant kernel (M = 4096, measured alone), the bitwise B=1-vs-B=N check and a CPU baseline.
 
---configs REPORT.json additionally runs the five BASELINE configs (BI check + throughput of
-every kernel family, and the reference's CPU path of each config on a bounded sample) and
-writes them to REPORT.json; the headline line is unchanged.
+The line's "configs" block covers all five BASELINE configs (skip with --no-configs): per
+config its bitwise batch-invariance check, its rate in TFLOP/s or GB/s with the fraction of
+the MI355X roofline that bounds it, the same call through stock torch on the GPU (mode off)
+with the reference's latency_ratio = invariant / stock
+(scripts/benchmark_batch_invariant_ops.py:44-65), and the reference's CPU path on a bounded
+sample.  --configs REPORT.json writes a longer report (materialised attention paths, dense
+MoE, larger row kernels).
 """
 
 from __future__ import annotations
@@ -138,7 +142,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--configs", default=None, help="also run the 5 BASELINE configs, write a JSON report")
+    p.add_argument("--configs", default=None, help="also write a longer report of the 5 BASELINE configs")
+    p.add_argument("--no-configs", action="store_true", help="leave the per-config block out of the line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
@@ -171,6 +176,36 @@ def event_time(fn, iters, blocks=5):
         end.synchronize()
         per_call.append(start.elapsed_time(end) / iters)
     per_call.sort()
+    return per_call[len(per_call) // 2]
+
+
+def graph_time(fn, calls=50, replays=5):
+    """Milliseconds per call of fn() with the host out of the way: `calls` calls captured in one
+    HIP graph, replayed `replays` times between HIP events (median replay / calls).  For kernels
+    shorter than the host's launch path, where back-to-back event timing measures the host."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    per_call = []
+    for _ in range(replays):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        per_call.append(start.elapsed_time(end) / calls)
+    per_call.sort()
+    del graph
     return per_call[len(per_call) // 2]
 
 
@@ -411,7 +446,7 @@ def run_all():
         return yn, yn.mean(-1), torch.linalg.vector_norm(yn, dim=-1)
 
     # The mode is switched on once around the stack, as a model would run under it: entering
-    # and leaving it registers and removes the nine overrides (timed on its own below).
+    # and leaving it registers and removes the ten overrides (timed on its own below).
     with bio.set_batch_invariant_mode():
         outs = {bsz: stack(x[:bsz]) for bsz in (1, 8, 32)}
     c2_bi = all(_bitwise(outs[bsz][i], outs[32][i][:bsz]) for bsz in (1, 8) for i in range(3))
@@ -576,6 +611,208 @@ def run_all():
     return report
 
 
+def config_block(cpu_seconds):
+    """The five BASELINE configs, compactly, for the headline line.  Per config: the bitwise
+    batch-invariance check the config states, the rate with its roofline fraction, the same
+    call through stock torch on this GPU (mode off) and latency_ratio = invariant / stock as
+    the reference reports it (scripts/benchmark_batch_invariant_ops.py:44-65), and the
+    reference's CPU path on a bounded sample (cpu_seconds per config; None: not run)."""
+    import torch
+    import torch.nn.functional as F
+
+    import batch_invariant_ops as bio
+    from batch_invariant_ops.moe import _moe
+
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    block = {}
+
+    def entry(bitwise, flops_or_bytes, ms, stock_ms, unit, peak, **extra):
+        rate = flops_or_bytes / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+        return {"bitwise": bitwise, "value": round(rate, 2), "unit": unit,
+                "frac_roofline": round(rate / peak, 4), "peak": peak, "ms": round(ms, 5),
+                "stock_ms": None if stock_ms is None else round(stock_ms, 5),
+                "latency_ratio": None if stock_ms is None else round(ms / stock_ms, 3), **extra}
+
+    # C1: the README fp32 check (README.md:62-76)
+    a = torch.linspace(-100, 100, 2048 * 4096, device=dev).reshape(2048, 4096)
+    b = torch.linspace(-100, 100, 4096 * 4096, device=dev).reshape(4096, 4096)
+    full = bio.matmul_persistent(a, b)
+    with bio.set_batch_invariant_mode():
+        bit = _bitwise(torch.mm(a[:1], b), full[:1]) and _bitwise(bio.matmul_persistent(a[:1], b), full[:1])
+    ms = event_time(lambda: bio.matmul_persistent(a, b), 10)
+    stock = event_time(lambda: torch.mm(a, b), 10)
+    block["C1"] = entry(bit, 2 * 2048 * 4096 * 4096, ms, stock, "TFLOP/s", PEAK_FP32_TFLOPS,
+                        workload="fp32 mm 2048x4096 . 4096x4096 (linspace); bitwise mm(A[:1],B) vs mm(A,B)[:1]")
+    del a, b, full
+
+    # C2: linear(+bias) -> linear -> HF RMSNorm (mean override) -> mean, L2 norm; B in {1, 8, 32}
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(32, 256, 2048, generator=g).to(bf).to(dev)
+    g = torch.Generator().manual_seed(20)
+    w1 = (torch.randn(8192, 2048, generator=g) * 0.02).to(bf).to(dev)
+    b1 = (torch.randn(8192, generator=g) * 0.02).to(bf).to(dev)
+    w2 = (torch.randn(2048, 8192, generator=g) * 0.02).to(bf).to(dev)
+
+    def stack(inp):
+        y = F.linear(F.linear(inp, w1, b1), w2)
+        var = y.float().pow(2).mean(-1, keepdim=True)
+        yn = (y.float() * torch.rsqrt(var + 1e-6)).to(bf)
+        return yn, yn.mean(-1), torch.linalg.vector_norm(yn, dim=-1)
+
+    with bio.set_batch_invariant_mode():
+        outs = {bsz: stack(x[:bsz]) for bsz in (1, 8, 32)}
+        inv = {bsz: event_time(lambda bsz=bsz: stack(x[:bsz]), 10) for bsz in (1, 8, 32)}
+    stock = {bsz: event_time(lambda bsz=bsz: stack(x[:bsz]), 10) for bsz in (1, 8, 32)}
+    bit = all(_bitwise(outs[bsz][i], outs[32][i][:bsz]) for bsz in (1, 8) for i in range(3))
+    c2 = entry(bit, 2 * 2 * 32 * 256 * 8192 * 2048, inv[32], stock[32], "TFLOP/s", PEAK_BF16_TFLOPS,
+               workload="bf16 stack at B=32 (M=8192): rate = the two linears' FLOPs / whole-stack time")
+    c2["stack_ms"] = {f"B{bsz}": round(inv[bsz], 5) for bsz in (1, 8, 32)}
+    c2["stock_stack_ms"] = {f"B{bsz}": round(stock[bsz], 5) for bsz in (1, 8, 32)}
+    yb = outs[32][0]
+    nbytes = yb.numel() * 2 + yb.numel() // 2048 * 2
+    for name, inv_fn, stock_fn in (
+            ("mean", lambda: bio.mean_dim(yb, -1), lambda: yb.mean(-1)),
+            ("l2_norm", lambda: bio.linalg_vector_norm_batch_invariant(yb, dim=-1),
+             lambda: torch.linalg.vector_norm(yb, dim=-1))):
+        ms_k, ms_s = graph_time(inv_fn), graph_time(stock_fn)
+        sub = entry(True, nbytes, ms_k, ms_s, "GB/s", PEAK_HBM_GBS,
+                    workload="[32,256,2048] bf16 over the last dim; time per call from a HIP graph of 50 calls")
+        sub["host_loop_ms"] = round(event_time(inv_fn, 50), 5)
+        c2[name] = sub
+    block["C2"] = c2
+    del x, w1, b1, w2, outs, yb
+
+    # C3: SDPA prefill, GQA 16/4, B = 16 (bits of B = 1 and 4 against B = 16)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(16, 16, 1024, 128, generator=g).to(bf).to(dev)
+    k = torch.randn(16, 4, 1024, 128, generator=g).to(bf).to(dev)
+    v = torch.randn(16, 4, 1024, 128, generator=g).to(bf).to(dev)
+    g = torch.Generator().manual_seed(30)
+    mask = torch.rand(16, 1, 1024, 1024, generator=g) * -10
+    mask[torch.rand(16, 1, 1024, 1024, generator=g) < 0.1] = -math.inf
+    mask = mask.to(bf).to(dev)
+    # stock attention: torch's fused kernels only (flash / memory-efficient), on K and V expanded
+    # to the query heads; torch's math fallback is kept out (its bf16 batched products take a
+    # transposed right operand)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    k16, v16 = k.repeat_interleave(4, 1), v.repeat_interleave(4, 1)
+
+    def stock_time(fn, reps):
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                fn()
+                return event_time(fn, reps)
+        except RuntimeError as exc:  # no fused torch kernel takes this call
+            print(f"stock attention unavailable: {exc}", file=sys.stderr, flush=True)
+            return None
+
+    for name, kw, pairs in (("C3_causal", {"is_causal": True}, 1024 * 1025 / 2),
+                            ("C3_mask", {"attn_mask": mask}, 1024 * 1024)):
+        def run(bsz, kw=kw):
+            kk = dict(kw)
+            if "attn_mask" in kk:
+                kk["attn_mask"] = kk["attn_mask"][:bsz]
+            return bio.scaled_dot_product_attention_batch_invariant(q[:bsz], k[:bsz], v[:bsz], enable_gqa=True, **kk)
+
+        o16 = run(16)
+        bit = _bitwise(run(1), o16[:1]) and _bitwise(run(4), o16[:4])
+        ms = event_time(lambda: run(16), 5)
+        stock = stock_time(lambda kw=kw: F.scaled_dot_product_attention(q, k16, v16, **kw), 5)
+        block[name] = entry(bit, 4 * 16 * 16 * pairs * 128, ms, stock, "TFLOP/s", PEAK_BF16_TFLOPS,
+                            workload="B=16, 16/4 heads, L=1024, D=128; useful FLOPs over the visible pairs")
+    del q, k, v, k16, v16, mask, o16
+
+    # C4: 32 packed sequences, bottom-right causal; stock = per-sequence SDPA calls
+    g = torch.Generator().manual_seed(4)
+    lengths = torch.randint(64, 2049, (32,), generator=g)
+    total = int(lengths.sum())
+    q = torch.randn(1, total, 8, 64, generator=g).to(bf).to(dev)
+    k = torch.randn(1, total, 2, 64, generator=g).to(bf).to(dev)
+    v = torch.randn(1, total, 2, 64, generator=g).to(bf).to(dev)
+    cu = torch.zeros(33, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lengths, 0)
+    cu_d = cu.to(dev)
+
+    def varlen():
+        return bio.varlen_scaled_dot_product_attention_batch_invariant(
+            q, k, v, cu_d, cu_d, is_causal=True, causal_type="BottomRight")
+
+    bounds = [(int(cu[i]), int(cu[i + 1])) for i in range(32)]
+    views = [(q[:, s0:s1].transpose(1, 2), k[:, s0:s1].transpose(1, 2).repeat_interleave(4, 1),
+              v[:, s0:s1].transpose(1, 2).repeat_interleave(4, 1)) for s0, s1 in bounds]
+
+    def per_sequence():
+        return [F.scaled_dot_product_attention(qq, kk, vv, is_causal=True) for qq, kk, vv in views]
+
+    packed = varlen()
+    bit = True
+    for s in range(32):
+        s0, s1 = bounds[s]
+        one = torch.tensor([0, s1 - s0], dtype=torch.int32, device=dev)
+        bit &= _bitwise(bio.varlen_scaled_dot_product_attention_batch_invariant(
+            q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], one, one, is_causal=True, causal_type="BottomRight"),
+            packed[:, s0:s1])
+    pairs = float((lengths.double() * (lengths.double() + 1) / 2).sum())
+    block["C4"] = entry(bit, 4 * 8 * 64 * pairs, event_time(varlen, 5), stock_time(per_sequence, 5), "TFLOP/s",
+                        PEAK_BF16_TFLOPS, workload=f"32 sequences ({total} tokens), 8/2 heads, D=64, per call "
+                        "(host offsets, plan, upload, kernel); every sequence alone vs packed; stock = one SDPA "
+                        "call per sequence")
+    del q, k, v, views, packed
+
+    # C5: top-8 SwiGLU MoE over 64 experts, T in {1, 256, 4096}; stock = the reference's dense
+    # every-expert evaluation (moe.py:75-91) on stock torch ops
+    g = torch.Generator().manual_seed(5)
+    hidden = torch.randn(4096, 2048, generator=g).to(bf).to(dev)
+    gu = (torch.randn(64, 2048, 1536, generator=g) * 0.02).to(bf).to(dev)
+    dn = (torch.randn(64, 768, 2048, generator=g) * 0.02).to(bf).to(dev)
+    wts, sel = torch.topk(torch.softmax(torch.randn(4096, 64, generator=g), -1), 8, dim=-1)
+    wts, sel = wts.to(dev), sel.to(dev)
+    gate, up, down = gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2), dn.transpose(1, 2)
+    gate_w, up_w, down_w = gu[..., :768].contiguous(), gu[..., 768:].contiguous(), dn  # [E,D,I], [E,I,D]
+
+    def moe(t):
+        return _moe(hidden[:t], wts[:t], sel[:t], gate, up, down, sparse=True)
+
+    def stock_moe(t):
+        xe = hidden[:t].unsqueeze(0).expand(64, -1, -1)
+        act = F.silu(torch.bmm(xe, gate_w)) * torch.bmm(xe, up_w)
+        y = torch.bmm(act, down_w).permute(1, 0, 2)
+        r = torch.gather(y, 1, sel[:t].unsqueeze(-1).expand(-1, -1, 2048)) * wts[:t].unsqueeze(-1).to(bf)
+        o = r[:, 0]
+        for s_ in range(1, 8):
+            o = o + r[:, s_]
+        return o
+
+    full = moe(4096)
+    by256 = torch.cat([_moe(hidden[t0:t0 + 256], wts[t0:t0 + 256], sel[t0:t0 + 256], gate, up, down, sparse=True)
+                       for t0 in range(0, 4096, 256)])
+    bit = _bitwise(by256, full) and all(
+        _bitwise(_moe(hidden[t:t + 1], wts[t:t + 1], sel[t:t + 1], gate, up, down, sparse=True), full[t:t + 1])
+        for t in range(0, 4096, 97))
+    for t in (1, 256, 4096):
+        reps = 3 if t == 4096 else 10
+        ms = event_time(lambda t=t: moe(t), reps)
+        stock = event_time(lambda t=t: stock_moe(t), reps)
+        block[f"C5_T{t}"] = entry(bit, 6 * 8 * t * 2048 * 768, ms, stock, "TFLOP/s", PEAK_BF16_TFLOPS,
+                                  workload=f"{t} tokens, hidden 2048, 64 experts, top-8, SwiGLU 768; FLOPs of the "
+                                  "selected routes; bitwise: batches of 256 and single tokens (every 97th) vs 4096")
+    del hidden, gu, dn, gate_w, up_w, full
+
+    if cpu_seconds:
+        cpu = cpu_config_baselines(cpu_seconds)
+        per = {"C1": ("C1_fp32_mm", "tflops"), "C2": ("C2_linear_rmsnorm", "gemm_tflops"),
+               "C3_causal": ("C3_sdpa", "tflops_useful"), "C4": ("C4_varlen", "tflops_useful"),
+               "C5_T256": ("C5_moe", "route_tflops")}
+        for key, (src, field) in per.items():
+            c = cpu[src]
+            block[key]["cpu"] = {"value": round(c[field], 4), "unit": "TFLOP/s", "cores": cpu["cores"],
+                                 "kind": "reference", "sample": c["sample"]}
+        block["cpu_host"] = {k_: cpu[k_] for k_ in ("cpu_model", "affinity_cpus", "torch", "cpu_capability")}
+    return block
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -680,6 +917,8 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if not args.no_configs:
+        line["configs"] = config_block(None if args.no_cpu else 2.0)
     if args.configs:
         report = run_all()
         if not args.no_cpu:
