@@ -639,6 +639,7 @@ def config_block(cpu_seconds):
     def entry(bitwise, flops_or_bytes, ms, stock_ms, unit, peak, **extra):
         rate = flops_or_bytes / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
         return {"bitwise": bitwise, "value": round(rate, 2), "unit": unit,
+                "bound": "hbm" if unit == "GB/s" else "mfma",
                 "frac_roofline": round(rate / peak, 4), "peak": peak, "ms": round(ms, 5),
                 "stock_ms": None if stock_ms is None else round(stock_ms, 5),
                 "latency_ratio": None if stock_ms is None else round(ms / stock_ms, 3), **extra}
@@ -816,13 +817,22 @@ def config_block(cpu_seconds):
     bit = _bitwise(by256, full) and all(
         _bitwise(_moe(hidden[t:t + 1], wts[t:t + 1], sel[t:t + 1], gate, up, down, sparse=True), full[t:t + 1])
         for t in range(0, 4096, 97))
+    expert_bytes = 3 * 2048 * 768 * 2
     for t in (1, 256, 4096):
         reps = 3 if t == 4096 else 10
         ms = event_time(lambda t=t: moe(t), reps)
         stock = event_time(lambda t=t: stock_moe(t), reps)
-        block[f"C5_T{t}"] = entry(bit, 6 * 8 * t * 2048 * 768, ms, stock, "TFLOP/s", PEAK_BF16_TFLOPS,
-                                  workload=f"{t} tokens, hidden 2048, 64 experts, top-8, SwiGLU 768; FLOPs of the "
-                                  "selected routes; bitwise: batches of 256 and single tokens (every 97th) vs 4096")
+        e = entry(bit, 6 * 8 * t * 2048 * 768, ms, stock, "TFLOP/s", PEAK_BF16_TFLOPS,
+                  workload=f"{t} tokens, hidden 2048, 64 experts, top-8, SwiGLU 768; FLOPs of the "
+                  "selected routes; bitwise: batches of 256 and single tokens (every 97th) vs 4096")
+        if t < 4096:
+            # few tokens: the call streams the weights of the experts it touches (HBM bound)
+            touched = int(torch.unique(sel[:t]).numel())
+            gbs = touched * expert_bytes / (ms * 1e-3) / 1e9
+            e["bound"] = "hbm"
+            e["touched_weight_GBs"] = round(gbs, 1)
+            e["frac_hbm"] = round(gbs / PEAK_HBM_GBS, 4)
+        block[f"C5_T{t}"] = e
     del hidden, gu, dn, gate_w, up_w, full
 
     if cpu_seconds:
