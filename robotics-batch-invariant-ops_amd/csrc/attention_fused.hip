@@ -100,7 +100,9 @@ struct FusedGeom {
 //          the chunk holds a multiple of 8 pairs, XCD x takes pairs x*n/8 .. (x+1)*n/8 - 1 of it
 //          at every level, so a head's key/value rows stay in one XCD's L2;
 //   varlen: the host sorts (sequence, query tile) entries by key range
-//          (biops_varlen_fused_order); the heads of an entry are consecutive tiles.
+//          (biops_varlen_fused_order); the heads of an entry are consecutive tiles, and in
+//          every chunk of kFusedChunk tiles XCD x takes the x-th eighth, so an entry's heads
+//          share one XCD's L2.
 constexpr int64_t kFusedChunk = 64;
 
 template <typename T, bool VARLEN>
@@ -108,6 +110,15 @@ __device__ __forceinline__ bool fused_geom(const FusedArgs& a, int64_t t, FusedG
   constexpr int E = sizeof(T);
   int64_t h, qt, qstart = 0, kstart = 0, b = 0;
   if constexpr (VARLEN) {
+    // Workgroup t runs XCD t % 8; in every chunk of kFusedChunk tiles (a multiple of 8), XCD x
+    // takes tiles x n/8 .. (x+1) n/8 - 1, the heads of one or a few consecutive entries, so a
+    // sequence's key/value rows are fetched into one XCD's L2 rather than into all eight.
+    {
+      const int64_t first = t / kFusedChunk * kFusedChunk;
+      const int64_t n = a.tiles - first < kFusedChunk ? a.tiles - first : kFusedChunk;
+      const int64_t j = t - first;
+      if ((n & 7) == 0) t = first + (j & 7) * (n >> 3) + (j >> 3);
+    }
     const int64_t e = a.order[t / a.hq];
     const int64_t item = e >> 32;
     qt = e & 0xffffffffLL;
