@@ -246,21 +246,27 @@ def _adversarial(kind, shape, seed, dtype):
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
 @pytest.mark.parametrize("kind", ("wide", "cancel", "tiny", "inf"))
 @pytest.mark.parametrize("m", (1, 20, 32))
-def test_skinny_entry_bits_on_adversarial_operands(tile_menu, dtype, kind, m):
-    """The skinny entry (16x16x32 MFMAs for 16-bit types) against entry 2 (32x32x16 MFMAs),
-    bit for bit, on operands that stress the accumulation: wide exponents, cancellation,
-    subnormal products and infinities (NaN results compare as equal only when both are NaN)."""
+@pytest.mark.parametrize("layout", ("kmajor", "nmajor"))
+@pytest.mark.parametrize("entry", ("skinny", 20, 21, 22))
+def test_16x16x32_entries_bits_on_adversarial_operands(tile_menu, dtype, kind, m, layout, entry):
+    """The entries that issue 16x16x32 MFMAs for 16-bit types -- the skinny entry and the
+    weight-streaming entries 20-22 (16-, 32- and 64-row m-tiles) -- against entry 2 (32x32x16
+    MFMAs), bit for bit, with K-major and N-major B, on operands that stress the accumulation:
+    wide exponents, cancellation, subnormal products and infinities (NaN results compare as
+    equal only when both are NaN)."""
+    if entry == "skinny" and layout == "nmajor":
+        pytest.skip("the skinny entry takes K-major B only (N-major calls go to another entry)")
     k, n = 4096, 1000
     x = gpu(_adversarial(kind, (m, k), 5400 + m, dtype))
     w = gpu(_adversarial(kind, (n, k), 5401, dtype))
+    b = w.t() if layout == "kmajor" else w.t().contiguous()
     assert tile_menu.biops_set_gemm_tile(2) == 0
     ref = matmul_persistent(x, w.t())
-    skinny = SKINNY_ENTRY
-    assert tile_menu.biops_set_gemm_tile(skinny) == 0
-    out = matmul_persistent(x, w.t())
+    assert tile_menu.biops_set_gemm_tile(SKINNY_ENTRY if entry == "skinny" else entry) == 0
+    out = matmul_persistent(x, b)
     both_nan = torch.isnan(out) & torch.isnan(ref)
     assert_bitwise(torch.where(both_nan, torch.zeros_like(out), out),
-                   torch.where(both_nan, torch.zeros_like(ref), ref), f"{kind}, m={m}")
+                   torch.where(both_nan, torch.zeros_like(ref), ref), f"entry {entry}, {layout}, {kind}, m={m}")
 
 
 @pytest.mark.parametrize(("m", "n", "bias"), (
