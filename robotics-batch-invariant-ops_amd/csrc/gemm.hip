@@ -500,8 +500,7 @@ static int launch_cfg(const BmmArgs& a0, hipStream_t stream) {
 template <typename T, int CFG, int EPI, bool GRP = false>
 static int launch_layout(const BmmArgs& a, bool b_kmajor, bool direct, hipStream_t s) {
   if (!b_kmajor) {
-    if constexpr (sizeof(T) == 2)
-      if (direct) return launch_cfg<T, CFG, false, true, EPI, GRP>(a, s);
+    if (direct) return launch_cfg<T, CFG, false, true, EPI, GRP>(a, s);
     return launch_cfg<T, CFG, false, false, EPI, GRP>(a, s);
   }
   if (direct) return launch_cfg<T, CFG, true, true, EPI, GRP>(a, s);
@@ -613,8 +612,8 @@ static int prepare_bmm(int dtype, BmmArgs& a, int epi, bool b_kmajor, bool& dire
   if (a.gB <= 0) a.gB = 1;
   if (a.nb2 <= 0) a.nb2 = 1;
   // Direct global->LDS loads need whole 16-byte chunks: aligned operands, K a multiple of the
-  // 128-byte step, and B K-major or (16-bit types) N-major with N a multiple of 8.
-  direct = a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) && (b_kmajor || (elt == 2 && a.N % 8 == 0)) &&
+  // 128-byte step, and B K-major or N-major with N a multiple of 16 / elt.
+  direct = a.a_vec && a.b_vec && ((a.K * elt) % kKBytes == 0) && (b_kmajor || (a.N * elt) % 16 == 0) &&
            !direct_disabled();
   // Grouped rows run on the table entries only (the skinny and large-tile kernels take a fixed
   // tile count from the host); those two read K-major B only.

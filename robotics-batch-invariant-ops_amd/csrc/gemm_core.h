@@ -129,6 +129,19 @@ template <int CPR>
 __device__ __forceinline__ int lds_off_n(int k, int col) {
   return k * CPR * 16 + ((((col >> 3) ^ nmajor_swz<CPR>(k))) << 4) + ((col & 7) << 1);
 }
+// N-major B stage (fp32): K row k holds the tile's CPR = BN/4 chunks of 4 columns, chunk c at
+// slot c ^ swz32(k).  Each fragment value is one 4-byte read: lanes 0-31 read 32 consecutive
+// columns of row k, lanes 32-63 the same columns of row k + 4, and swz32 puts those two rows in
+// opposite 128-byte halves of the banks (for CPR >= 16: rows of 256 bytes or more).
+template <int CPR>
+__device__ __forceinline__ int nmajor32_swz(int k) {
+  if constexpr (CPR >= 16) return ((k >> 2) & 1) << 3;
+  else return 0;
+}
+template <int CPR>
+__device__ __forceinline__ int lds_off_n32(int k, int col) {
+  return k * CPR * 16 + ((((col >> 2) ^ nmajor32_swz<CPR>(k))) << 4) + ((col & 3) << 2);
+}
 typedef short tr16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) tr16x4_t lds_tr16x4_t;
 __device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
@@ -155,8 +168,8 @@ __device__ __forceinline__ void lds_wait_anchor(u32x2_t& x, u32x2_t& y) {
 // Block tile BM x BN computed by WGM x WGN wavefronts (each WM x WN = FM x FN 32x32 blocks);
 // LW further wavefronts only issue loads (more bytes in flight per workgroup: a wavefront keeps at
 // most 63 vector-memory operations outstanding).  STAGES LDS buffers form a ring.  DIRECT: operands go global -> LDS by global_load_lds_dwordx4
-// (16-byte aligned rows, K a multiple of the step; B K-major, or N-major for 16-bit types with
-// whole 8-column chunks); otherwise through registers.
+// (16-byte aligned rows, K a multiple of the step; B K-major, or N-major with whole 16-byte
+// chunks of columns); otherwise through registers.
 template <typename T, int BM, int BN, int WGM, int WGN, int STAGES, bool B_KMAJOR, bool DIRECT, int LW = 0>
 struct GemmTile {
   static constexpr int THREADS = 64 * (WGM * WGN + LW);
@@ -182,8 +195,12 @@ struct GemmTile {
   static constexpr int BN_LOADS = (BN_BLOCKS + THREADS - 1) / THREADS;
   static constexpr int B_REGS = B_KMAJOR ? B_LOADS : 4 * BN_LOADS;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert(!DIRECT || B_KMAJOR || sizeof(T) == 2, "N-major direct loads: 16-bit types");
   static constexpr int CPR_N = BN / VEC;  // chunks per K row of an N-major B stage
+  // slot of chunk c in K row k of an N-major B stage (an involution on 0 .. CPR_N - 1)
+  __device__ static __forceinline__ int nmajor_slot(int k, int c) {
+    if constexpr (sizeof(T) == 4) return c ^ nmajor32_swz<CPR_N>(k);
+    else return c ^ nmajor_swz<CPR_N>(k);
+  }
   static_assert(!DIRECT || (A_SLOTS % THREADS == 0 && B_SLOTS % THREADS == 0), "direct split");
   static_assert(STAGES >= 2, "at least two stages");
   static constexpr int LOADS_PER_STAGE = A_LOADS + B_LOADS;  // direct path, per thread
@@ -367,13 +384,13 @@ struct GemmTile {
                                          (lds_void_t*)(Bs + (THREADS * p + wbase) * 16), 16, 0, 0);
       }
     } else {
-      // Slot s: K row s / CPR_N, slot s % CPR_N holding chunk (slot) ^ swz(row) of 8 columns;
-      // chunks past the last column re-load the last whole chunk (never stored).
+      // Slot s: K row s / CPR_N, slot s % CPR_N holding chunk nmajor_slot(row, slot) of VEC
+      // columns; chunks past the last column re-load the last whole chunk (never stored).
 #pragma unroll
       for (int p = 0; p < B_SLOTS / THREADS; ++p) {
         const int s = t + THREADS * p;
         const int k = s / CPR_N;
-        const int c = (s % CPR_N) ^ nmajor_swz<CPR_N>(k);
+        const int c = nmajor_slot(k, s % CPR_N);
         int64_t local;
         const T* base = B.col_base(c * VEC, local);
         if (local >= B.ncols) local = B.ncols - VEC;
@@ -397,6 +414,15 @@ struct GemmTile {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         b[j] = *reinterpret_cast<const u32x4_t*>(stage + LDS_A + lds_off(wn * WN + j * 32 + lr, 2 * q + lb));
+    } else if constexpr (sizeof(T) == 4) {
+      // fp32 N-major: value e of the fragment is K row 8q + 4lb + e (the K index the K-major
+      // chunk 2q + lb holds in element e) of column wn*WN + 32j + lr
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          b[j][e] = *reinterpret_cast<const uint32_t*>(
+              stage + LDS_A + lds_off_n32<CPR_N>(8 * q + 4 * lb + e, wn * WN + j * 32 + lr));
     } else {
       (void)wn;
       TrHalves h;
@@ -438,7 +464,7 @@ struct GemmTile {
     u32x4_t b[2][FN];
   };
   __device__ static __forceinline__ void load_group(const char* stage, int g, Frags& f) {
-    if constexpr (DIRECT && !B_KMAJOR) {
+    if constexpr (DIRECT && !B_KMAJOR && sizeof(T) == 2) {
       // both steps' reads go out before the one wait
       const int lane = threadIdx.x & 63;
       const int wm = (threadIdx.x >> 6) / WGN;

@@ -320,7 +320,7 @@ def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
     assert_bitwise(matmul_persistent(x, w.t()), ref_plain, "skinny entry, no bias")
 
 
-@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 @pytest.mark.parametrize(("m", "k", "n"), (
     (300, 2048, 520),   # N-major direct loads, partial last column tile
     (77, 1024, 256),
@@ -328,7 +328,8 @@ def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
     (130, 128, 1000),   # N % 256 != 0: clamped chunks in the last tile
     (64, 4096, 24),
     (513, 192, 264),
-    (40, 256, 100),     # N % 8 != 0: register path
+    (40, 256, 100),     # N % 8 != 0: register path for 16-bit types, fp32 direct
+    (33, 256, 98),      # N % 4 != 0: register path for every type
 ))
 def test_nmajor_b_matches_kmajor_bits(tile_menu, dtype, m, k, n):
     """Row-major B (N-major: global->LDS loads and transposing LDS reads when whole 8-column
