@@ -852,8 +852,9 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(
-            f"bench.py runs on exactly one GPU (asked for {args.gpus}): this build's hot path is "
-            "single-GPU; see DESIGN.md for how it would shard.",
+            f"bench.py runs on exactly one GPU (asked for {args.gpus}): the operators work on one "
+            "GPU's share of a job (a data-parallel rank's rows, a tensor-parallel rank's columns), "
+            "and no multi-GPU figure is measured here.",
             file=sys.stderr,
         )
         sys.exit(2)
