@@ -115,6 +115,12 @@ def profile_kernel(which, iters):
         x = torch.randn(1024, k, generator=g).to(torch.bfloat16).cuda()
         for _ in range(iters):
             linear_batch_invariant(x, w)
+    elif which == "c1":
+        # the README's fp32 mm, 2048x4096 . 4096x4096 (linspace operands, B row-major)
+        a = torch.linspace(-100, 100, 2048 * 4096, device="cuda").reshape(2048, 4096)
+        b = torch.linspace(-100, 100, 4096 * 4096, device="cuda").reshape(4096, 4096)
+        for _ in range(iters):
+            bio.matmul_persistent(a, b)
     elif which == "softmax":
         x = torch.randn(16 * 16 * 1024, 1024, device="cuda").to(torch.bfloat16)
         for _ in range(iters):
@@ -155,11 +161,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "gemm_mid", "copy", "sdpa", "varlen", "moe", "moe_t1", "softmax", "norm", "mean_c2",
+        choices=("gemm", "gemm_mid", "copy", "c1", "sdpa", "varlen", "moe", "moe_t1", "softmax", "norm", "mean_c2",
                  "norm_c2"),
         default=None,
         help="only launch the roofline kernel (gemm), the M=1024 8192->2048 linear (gemm_mid), a "
-        "512 MiB device copy (copy), configs[2] causal attention at B=16 (sdpa), configs[3] varlen "
+        "512 MiB device copy (copy), configs[0]'s fp32 mm (c1), configs[2] causal attention at B=16 (sdpa), configs[3] varlen "
         "attention (varlen), configs[4] MoE at T=4096 (moe) or T=1 (moe_t1), a 262144x1024 bf16 softmax (softmax), "
         "a 65536x2048 bf16 row L2 norm (norm) or configs[1]'s mean / L2 norm over [32,256,2048] bf16 (mean_c2, "
         "norm_c2) --iters times, for counter runs; prints no JSON line",
