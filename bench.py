@@ -75,9 +75,9 @@ def profile_kernel(which, iters):
         v = torch.randn(16, 4, 1024, 128, generator=g).to(torch.bfloat16).cuda()
         for _ in range(iters):
             bio.scaled_dot_product_attention_batch_invariant(q, k, v, is_causal=True, enable_gqa=True)
-    elif which in ("moe", "moe_t1"):
-        # configs[4] at T = 4096 (moe) or its first token alone (moe_t1, the one-token split of
-        # the config), selected routes (the default evaluation)
+    elif which in ("moe", "moe_t1", "moe_t256"):
+        # configs[4] at T = 4096 (moe), its first 256 tokens (moe_t256) or its first token alone
+        # (moe_t1), the splits of the config; selected routes (the default evaluation)
         from batch_invariant_ops.moe import _moe
 
         g = torch.Generator().manual_seed(5)
@@ -87,7 +87,7 @@ def profile_kernel(which, iters):
         probs = torch.softmax(torch.randn(4096, 64, generator=g), -1)
         wts, sel = torch.topk(probs, 8, dim=-1)
         wts, sel = wts.cuda(), sel.cuda()
-        t = 1 if which == "moe_t1" else 4096
+        t = {"moe_t1": 1, "moe_t256": 256}.get(which, 4096)
         for _ in range(iters):
             _moe(hidden[:t], wts[:t], sel[:t], gu[..., :768].transpose(1, 2), gu[..., 768:].transpose(1, 2),
                  dn.transpose(1, 2), sparse=True)
@@ -161,12 +161,13 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "gemm_mid", "copy", "c1", "sdpa", "varlen", "moe", "moe_t1", "softmax", "norm", "mean_c2",
-                 "norm_c2"),
+        choices=("gemm", "gemm_mid", "copy", "c1", "sdpa", "varlen", "moe", "moe_t1", "moe_t256", "softmax", "norm",
+                 "mean_c2", "norm_c2"),
         default=None,
         help="only launch the roofline kernel (gemm), the M=1024 8192->2048 linear (gemm_mid), a "
         "512 MiB device copy (copy), configs[0]'s fp32 mm (c1), configs[2] causal attention at B=16 (sdpa), configs[3] varlen "
-        "attention (varlen), configs[4] MoE at T=4096 (moe) or T=1 (moe_t1), a 262144x1024 bf16 softmax (softmax), "
+        "attention (varlen), configs[4] MoE at T=4096 (moe), T=256 (moe_t256) or T=1 (moe_t1), a 262144x1024 bf16 "
+        "softmax (softmax), "
         "a 65536x2048 bf16 row L2 norm (norm) or configs[1]'s mean / L2 norm over [32,256,2048] bf16 (mean_c2, "
         "norm_c2) --iters times, for counter runs; prints no JSON line",
     )

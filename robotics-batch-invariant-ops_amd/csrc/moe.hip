@@ -404,40 +404,55 @@ __global__ __launch_bounds__(256) void moe_route_rows_kernel(PackArgs a) {
 // bucket b's count per wavefront goes to LDS; thread b then turns the 16 counts into the routes
 // of earlier wavefronts, and a workgroup scan over the buckets places rows and m-tiles.
 // The workgroup has the fewest of 2 / 4 / 8 / 16 wavefronts that give every route and every
-// bucket a thread.
-constexpr int kSmallPackRoutes = 1024;  // routes (one per thread)
+// bucket a thread.  Calls of up to 4096 routes over at most 127 experts take the same kernel
+// with 16 wavefronts and up to four passes over the routes: pass p gives thread t route
+// 1024 p + t, and the per-wavefront counts of every pass are prefixed in route order.
+constexpr int kSmallPackRoutes = 1024;  // routes per pass (one per thread)
 constexpr int kSmallPackBuckets = 512;  // experts + 1 (the bucket of invalid indices)
+constexpr int kMultiPackPasses = 4;     // passes of the multi-pass form
+constexpr int kMultiPackBuckets = 128;  // its experts + 1
 
-template <int WAVES>
+template <int WAVES, int PASSES = 1, int BUCKETS = kSmallPackBuckets>
 __global__ __launch_bounds__(WAVES * 64) void moe_pack_small_kernel(PackArgs a) {
-  static_assert(WAVES * 64 <= kSmallPackRoutes, "one thread per route");
-  __shared__ int32_t cnt[WAVES][kSmallPackBuckets];
-  __shared__ int32_t first_row[kSmallPackBuckets];
+  constexpr int NT = WAVES * 64;
+  static_assert(NT <= kSmallPackRoutes, "one thread per route of a pass");
+  static_assert(PASSES == 1 || BUCKETS <= NT, "one thread per bucket (the launcher checks it otherwise)");
+  // row v = p * WAVES + w: counts of wavefront w in pass p (route order)
+  __shared__ int32_t cnt[PASSES * WAVES][BUCKETS];
+  __shared__ int32_t first_row[BUCKETS];
   __shared__ int32_t wsum[WAVES][3];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int E = (int)a.E, E1 = E + 1;
-  for (int b = lane; b < E1; b += 64) cnt[w][b] = 0;
-  const bool valid = tid < a.R;
-  int bucket = E;
-  if (valid) {
-    const int64_t e = a.sel[tid];
-    if (e >= 0 && e < a.E) bucket = (int)e;
-  }
+  // each wavefront zeroes and writes only its own rows of cnt
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p)
+    for (int b = lane; b < E1; b += 64) cnt[p * WAVES + w][b] = 0;
   const int nbits = 32 - __clz(E);
-  uint64_t same = __ballot(valid);
-  for (int bit = 0; bit < nbits; ++bit) {
-    const bool on = (bucket >> bit) & 1;
-    const uint64_t m = __ballot(valid && on);
-    same &= on ? m : ~m;
-  }
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  const int lower = __popcll(same & below);
-  // each wavefront writes only its own row of cnt (zeroed above by the same wavefront)
-  if (valid && lower == 0) cnt[w][bucket] = __popcll(same);
+  bool valid[PASSES];
+  int bucket[PASSES], lower[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int64_t r = (int64_t)p * NT + tid;
+    valid[p] = r < a.R;
+    bucket[p] = E;
+    if (valid[p]) {
+      const int64_t e = a.sel[r];
+      if (e >= 0 && e < a.E) bucket[p] = (int)e;
+    }
+    uint64_t same = __ballot(valid[p]);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (bucket[p] >> bit) & 1;
+      const uint64_t m = __ballot(valid[p] && on);
+      same &= on ? m : ~m;
+    }
+    lower[p] = __popcll(same & below);
+    if (valid[p] && lower[p] == 0) cnt[p * WAVES + w][bucket[p]] = __popcll(same);
+  }
   lds_sync();
   int32_t n = 0;  // routes of bucket tid
   if (tid < E1) {
-    for (int v = 0; v < WAVES; ++v) {
+    for (int v = 0; v < PASSES * WAVES; ++v) {
       const int32_t c = cnt[v][tid];
       cnt[v][tid] = n;
       n += c;
@@ -482,13 +497,17 @@ __global__ __launch_bounds__(WAVES * 64) void moe_pack_small_kernel(PackArgs a) 
     a.grp2[0] = p2 + i2;
   }
   lds_sync();
-  if (valid) {
-    int32_t row = -1;
-    if (bucket < E) {
-      row = first_row[bucket] + cnt[w][bucket] + lower;
-      a.row_token[row] = (int32_t)(tid / a.k);
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    if (valid[p]) {
+      const int64_t r = (int64_t)p * NT + tid;
+      int32_t row = -1;
+      if (bucket[p] < E) {
+        row = first_row[bucket[p]] + cnt[p * WAVES + w][bucket[p]] + lower[p];
+        a.row_token[row] = (int32_t)(r / a.k);
+      }
+      a.route_row[r] = row;
     }
-    a.route_row[tid] = row;
   }
 }
 
@@ -705,12 +724,23 @@ static int moe_sparse_run(int dtype, int64_t tokens, int64_t experts, int64_t hi
     // Tail m-tiles go to separate launches on the weight-streaming tile (plan kernel path).
     p.tail1 = small ? 0 : grouped_tail_rows(dtype, g.gu, kEpiSwiglu, g.gu_kmajor);
     p.tail2 = small ? 0 : grouped_tail_rows(dtype, g.dn, kEpiPlain, g.dn_kmajor);
+    // up to 4096 routes over at most 127 experts without tails: the multi-pass one-workgroup
+    // packing (C5 at 256 tokens: one kernel of about 5 us against the three of the plan path)
+    const bool multi = !small && R <= (int64_t)kMultiPackPasses * kSmallPackRoutes &&
+                       experts + 1 <= kMultiPackBuckets && p.tail1 == 0 && p.tail2 == 0;
     if (small) {
       const int64_t threads = std::max<int64_t>(R, experts + 1);
       if (threads <= 128) hipLaunchKernelGGL(moe_pack_small_kernel<2>, dim3(1), dim3(128), 0, s, p);
       else if (threads <= 256) hipLaunchKernelGGL(moe_pack_small_kernel<4>, dim3(1), dim3(256), 0, s, p);
       else if (threads <= 512) hipLaunchKernelGGL(moe_pack_small_kernel<8>, dim3(1), dim3(512), 0, s, p);
       else hipLaunchKernelGGL(moe_pack_small_kernel<16>, dim3(1), dim3(1024), 0, s, p);
+      if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
+    } else if (multi) {
+      if (R <= 2 * kSmallPackRoutes)
+        hipLaunchKernelGGL((moe_pack_small_kernel<16, 2, kMultiPackBuckets>), dim3(1), dim3(1024), 0, s, p);
+      else
+        hipLaunchKernelGGL((moe_pack_small_kernel<16, kMultiPackPasses, kMultiPackBuckets>), dim3(1), dim3(1024), 0,
+                           s, p);
       if ((rc = check_launch("moe_pack_small_kernel")) != BIOPS_OK) return rc;
     } else {
       const size_t hist_bytes = (size_t)kRankWaves * (experts + 1) * sizeof(int32_t);

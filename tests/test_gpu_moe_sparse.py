@@ -218,11 +218,13 @@ def test_stream_entries_equal_dense(dtype, T, E, D, I, k):
         lib.biops_set_gemm_tile(-1)
 
 
-@pytest.mark.parametrize("T,E,k", [(1, 64, 8), (128, 64, 8), (129, 64, 8), (4096, 64, 8), (3, 511, 4), (3, 512, 4)])
+@pytest.mark.parametrize("T,E,k", [(1, 64, 8), (128, 64, 8), (129, 64, 8), (200, 64, 8), (256, 64, 8), (512, 64, 8),
+                                   (513, 64, 8), (300, 127, 8), (300, 128, 8), (4096, 64, 8), (3, 511, 4), (3, 512, 4)])
 def test_one_workgroup_packing_limits(quiet_index_watch, T, E, k):
-    """Up to 1024 routes and 511 experts the routes are packed by one workgroup, beyond by the
-    rank / plan / route-row kernels: both sides of each limit give the dense path's bits,
-    with an out-of-range index among the routes."""
+    """Up to 1024 routes and 511 experts the routes are packed by one workgroup in one pass, up
+    to 4096 routes and 127 experts in two or four passes, beyond by the rank / plan / route-row
+    kernels: both sides of each limit give the dense path's bits, with an out-of-range index
+    among the routes."""
     D, I = 64, 64
     hidden = randn(T, D, seed=7740 + T, dtype=torch.bfloat16).cuda()
     gate, up, down = nmajor_weights(E, I, D, 7741, torch.bfloat16)
