@@ -273,7 +273,9 @@ static const double kCfgRate[kNumCfg] = {950, 750, 820, 450, 520, 330, 400, 180,
 // on MI355X (M = 4096 x N = 8192 / 2048 x K = 2048 / 8192 and 2048 x 1536 x 2048) while the
 // compiler still drained the global->LDS loads before those reads; re-measured without that
 // drain the large entries keep 0.94-1.0, but the older shares pick the faster entries for the
-// MoE expert GEMMs (4096 tokens: 553 us per call against 598 us), so they are kept.
+// MoE expert GEMMs (4096 tokens: 553 us per call against 598 us), so they are kept.  An fp32
+// N-major B on the direct path (one 4-byte LDS read per fragment value) is costed at the
+// K-major rate: it measured within 1 % of K-major on every entry (2048 x 4096 x 4096).
 static const double kCfgNmajorShare[kNumCfg] = {0.97, 0.78, 0.86, 0.60, 0.72, 0.60, 0.55, 0.60, 0.73, 0.78, 0.80, 0.83};
 static const int kCfgBM[kNumCfg] = {256, 256, 128, 128, 64, 32, 32, 32, 128, 128, 256, 128};
 static const int kCfgBN[kNumCfg] = {256, 128, 128, 64, 64, 64, 32, 64, 128, 256, 128, 256};
