@@ -149,6 +149,21 @@ def test_bmm_matches_oracle_for_noncontiguous_attention_inputs(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_bmm_row_major_b_on_the_direct_path(dtype):
+    """Row-major (N-major) right operands whose K is a whole number of 128-byte steps and whose
+    rows are whole 16-byte chunks take the global->LDS path for every dtype (fp32 with 4-byte
+    fragment reads): oracle parity, and the bits of the same values stored K-major."""
+    a = randn(3, 70, 256, seed=4200, dtype=dtype)
+    b = randn(3, 256, 104, seed=4201, dtype=dtype)
+    out = bmm_persistent(*gpu(a, b))
+    assert_gemm_close(out, oracle.bmm(a, b), a.double().abs() @ b.double().abs(), 256)
+    b_kmajor = gpu(b).transpose(1, 2).contiguous().transpose(1, 2)
+    assert b_kmajor.stride(1) == 1
+    assert_bitwise(bmm_persistent(gpu(a), b_kmajor), out, "K-major B")
+    assert_first_sample_equal(bmm_persistent(gpu(a)[:1], gpu(b)[:1]), out)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_bmm_broadcast_operand_matches_oracle(dtype):
     """Stride-0 batch operand (the MoE token matrix) and a row-major right operand."""
     x = randn(19, 40, seed=4100, dtype=dtype)
