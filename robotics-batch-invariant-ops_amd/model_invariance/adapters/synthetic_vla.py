@@ -7,8 +7,6 @@ model runs on the first ROCm GPU (CPU when there is none, for the harness's own 
 
 from __future__ import annotations
 
-import math
-
 import torch
 import torch.nn.functional as F
 

@@ -13,12 +13,11 @@ and both sides of the limits of the one-workgroup packing.
 import pytest
 import torch
 
-import oracle
 from batch_invariant_ops import _native as nat
 from batch_invariant_ops.moe import _IndexWatch, _moe, check_moe_indices
 
 from _parity import check_moe
-from _tol import ULP, assert_bitwise, assert_close_scaled
+from _tol import assert_bitwise
 
 pytestmark = pytest.mark.gpu
 

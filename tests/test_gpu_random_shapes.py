@@ -6,7 +6,6 @@ Shapes are drawn with a fixed seed (deterministic test) from ranges that cross t
 block boundaries of every kernel: rows and columns not multiples of 32/64/128, K not a multiple
 of the 128-byte step, head sizes on and off the fused-attention envelope."""
 
-import math
 import random
 
 import pytest

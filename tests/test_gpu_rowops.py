@@ -10,7 +10,6 @@ import torch.nn.functional as F
 import oracle
 from batch_invariant_ops import (
     linalg_vector_norm_batch_invariant,
-    log_softmax,
     mean_dim,
     set_batch_invariant_mode,
     softmax,
