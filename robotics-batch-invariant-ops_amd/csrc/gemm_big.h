@@ -26,7 +26,8 @@
 // MFMAs only read fragments loaded during the previous group.
 // K-major blocks from 128 x 128 up take two pairs per group instead (group A: pairs 0, 1 with
 // the reads of pairs 2, 3; group B: wait, barrier, the reads of pairs 0, 1 of stage h+1, pairs
-// 2, 3 with the refill), so that a read has two pairs of MFMAs to land, not one.  Measured on
+// 2, 3 with the refill, half of it after pair 2's reads where the 256 x 256 block leaves MFMAs
+// there), so that a read has two pairs of MFMAs to land, not one.  Measured on
 // MI355X (same-box A/B, the two kernels timed in alternating order, bitwise-identical outputs):
 // 256 x 256 at M = 4096, N = 8192, K = 2048 114.5 -> 113.0 us and K = 8192 378.2 -> 373.8 us;
 // 256 x 128 at 4096 x 2048 x 8192 110.1 -> 107.5 us; 128 x 128 at 2048 x 2048 x 8192
@@ -219,12 +220,14 @@ struct BigTile {
     __builtin_amdgcn_global_load_lds((global_cvoid_t*)ptr,
                                      (lds_void_t*)(smem + slot * LDS_STAGE + (THREADS * p + wbase) * 16), 16, 0, 0);
   }
-  // The MFMAs of one pair with the loads of a stage interleaved: MFMA q is followed by loads
-  // [q * LOADS / NM, (q + 1) * LOADS / NM).  A burst of loads ahead of the MFMAs (each load
-  // sets M0 and its address first) leaves the MFMA pipe idle: interleaving measured -4 % at
-  // 256 x 256, M = 4096, N = 8192, K = 2048 and 8192.
+  // The MFMAs of one pair with loads [P0, P1) of a stage interleaved: MFMA q is followed by
+  // loads P0 + [q * n / NM, (q + 1) * n / NM), n = P1 - P0.  A burst of loads ahead of the
+  // MFMAs (each load sets M0 and its address first) leaves the MFMA pipe idle: interleaving
+  // measured -4 % at 256 x 256, M = 4096, N = 8192, K = 2048 and 8192.
+  template <int P0, int P1>
   __device__ static __forceinline__ void mfmas_loads(Acc (&acc)[FM][FN], const Frags& f, char* smem,
                                                      const Src& src, int slot, int64_t k) {
+    constexpr int n = P1 - P0;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -232,23 +235,31 @@ struct BigTile {
         Mfma<T>::step(acc[i][j], f.a[i], f.b[j]);
         const int q = i * FN + j;
 #pragma unroll
-        for (int p = q * LOADS / NM; p < (q + 1) * LOADS / NM; ++p) issue_one(smem, src, slot, k, p);
+        for (int p = P0 + q * n / NM; p < P0 + (q + 1) * n / NM; ++p) issue_one(smem, src, slot, k, p);
       }
-    sched_loads<0>();
+    sched_loads<0, n>();
   }
-  template <int Q>
+  // Schedule of NMF MFMAs, each followed by its share of n loads.
+  template <int Q, int n, int NMF = NM>
   __device__ static __forceinline__ void sched_loads() {
-    if constexpr (Q < NM) {
-      constexpr int n = (Q + 1) * LOADS / NM - Q * LOADS / NM;
+    if constexpr (Q < NMF) {
+      constexpr int c = (Q + 1) * n / NMF - Q * n / NMF;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // MFMA
-      if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);  // VMEM
-      sched_loads<Q + 1>();
+      if constexpr (c > 0) __builtin_amdgcn_sched_group_barrier(0x020, c, 0);  // VMEM
+      sched_loads<Q + 1, n, NMF>();
     }
   }
 
   // Two pairs per group when a group's reads fit after the first pair's first MFMAs (two reads
   // after each).
   static constexpr bool TWO_PAIR = BKM && (FM + FN) <= NM;
+  // Refill loads of a stage that go with the MFMAs of pair 2 after its reads (FM + FN MFMAs
+  // carry the reads), where those remaining MFMAs can take one load each: half the loads; the
+  // rest go with pair 3.  Measured on MI355X (same-box A/B, alternating order, bitwise-equal
+  // outputs), 256 x 256: M = 4096, N = 8192, K = 2048 121.5 -> 119.0 us, 8192^3 845.5 ->
+  // 818.6 us; 128 x 128 blocks (no MFMA of pair 2 left after its reads) keep every load with
+  // pair 3, where moving them measured slower (2048 x 2048 x 8192 69.4 -> 71.6 us).
+  static constexpr int LOADS_P2 = NM - (FM + FN) >= LOADS / 2 ? LOADS / 2 : 0;
   struct Frags2 {
     Frags f[2];
   };
@@ -290,8 +301,12 @@ struct BigTile {
       lds_barrier();
       read2(smem + nxt * LDS_STAGE, 0, F[0]);
       mfmas(acc, F[1].f[0]);
-      interleave2<NM>();
-      mfmas_loads(acc, F[1].f[1], smem, src, cur, stage_k(h + STAGES));
+#pragma unroll
+      for (int p = 0; p < LOADS_P2; ++p) issue_one(smem, src, cur, stage_k(h + STAGES), p);
+      interleave2<FM + FN>();
+      sched_loads<0, LOADS_P2, NM - (FM + FN)>();
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas_loads<LOADS_P2, LOADS>(acc, F[1].f[1], smem, src, cur, stage_k(h + STAGES));
       __builtin_amdgcn_sched_barrier(0);
       cur = nxt;
     }
@@ -350,7 +365,7 @@ struct BigTile {
           wait_loads<(STAGES - 2) * LOADS>();
           lds_barrier();
           read_frags(smem + nxt * LDS_STAGE, 0, next);
-          mfmas_loads(acc, use, smem, src, cur, stage_k(h + STAGES));
+          mfmas_loads<0, LOADS>(acc, use, smem, src, cur, stage_k(h + STAGES));
           __builtin_amdgcn_sched_barrier(0);
         }
       }
