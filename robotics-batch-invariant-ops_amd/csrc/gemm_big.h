@@ -26,8 +26,8 @@
 // MFMAs only read fragments loaded during the previous group.
 // K-major blocks from 128 x 128 up take two pairs per group instead (group A: pairs 0, 1 with
 // the reads of pairs 2, 3; group B: wait, barrier, the reads of pairs 0, 1 of stage h+1, pairs
-// 2, 3 with the refill, half of it after pair 2's reads where the 256 x 256 block leaves MFMAs
-// there), so that a read has two pairs of MFMAs to land, not one.  Measured on
+// 2, 3 with the refill, part of it after pair 2's reads where MFMAs of pair 2 remain there),
+// so that a read has two pairs of MFMAs to land, not one.  Measured on
 // MI355X (same-box A/B, the two kernels timed in alternating order, bitwise-identical outputs):
 // 256 x 256 at M = 4096, N = 8192, K = 2048 114.5 -> 113.0 us and K = 8192 378.2 -> 373.8 us;
 // 256 x 128 at 4096 x 2048 x 8192 110.1 -> 107.5 us; 128 x 128 at 2048 x 2048 x 8192
@@ -254,12 +254,13 @@ struct BigTile {
   // after each).
   static constexpr bool TWO_PAIR = BKM && (FM + FN) <= NM;
   // Refill loads of a stage that go with the MFMAs of pair 2 after its reads (FM + FN MFMAs
-  // carry the reads), where those remaining MFMAs can take one load each: half the loads; the
-  // rest go with pair 3.  Measured on MI355X (same-box A/B, alternating order, bitwise-equal
-  // outputs), 256 x 256: M = 4096, N = 8192, K = 2048 121.5 -> 119.0 us, 8192^3 845.5 ->
-  // 818.6 us; 128 x 128 blocks (no MFMA of pair 2 left after its reads) keep every load with
-  // pair 3, where moving them measured slower (2048 x 2048 x 8192 69.4 -> 71.6 us).
-  static constexpr int LOADS_P2 = NM - (FM + FN) >= LOADS / 2 ? LOADS / 2 : 0;
+  // carry the reads): one per remaining MFMA, at most half the loads; the rest go with pair 3.
+  // Measured on MI355X (same-box A/B, alternating order, bitwise-equal outputs): 256 x 256 (8
+  // of 16 loads) at M = 4096, N = 8192, K = 2048 121.5 -> 119.0 us, 8192^3 845.5 -> 818.6 us;
+  // 256 x 128 (2 of 12) at 4096 x 2048 x 8192 122.2 -> 120.4 us.  128 x 128 blocks have no MFMA
+  // of pair 2 left after its reads and keep every load with pair 3 (all 8 after pair 2's
+  // MFMAs measured slower there: 2048 x 2048 x 8192 69.4 -> 71.6 us).
+  static constexpr int LOADS_P2 = NM - (FM + FN) < LOADS / 2 ? NM - (FM + FN) : LOADS / 2;
   struct Frags2 {
     Frags f[2];
   };
