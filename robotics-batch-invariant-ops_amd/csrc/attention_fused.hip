@@ -185,11 +185,13 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
   else return (uint32_t)Num<T>::to_bits(x) | ((uint32_t)Num<T>::to_bits(y) << 16);
 }
 
-// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Two wavefronts per SIMD
-// up to head size 128; with a 256-wide head (Q fragments and O accumulators twice as large,
-// 128 KiB of K/V blocks) one wavefront per SIMD with the full register file.
+// MASK: 0 none, 1 boolean (bytes, nonzero = keep), 2 additive (T).  Wavefronts per SIMD: three
+// with head sizes up to 64 (154-167 registers, 32 KiB of K/V blocks per workgroup; C4's varlen
+// call, MI355X, same-box A/B: 157.7 -> 138.1 us, same bits), two up to 128 (the mixed 64 / 128
+// heads spill at three), and with a 256-wide head (Q fragments and O accumulators twice as
+// large, 128 KiB of K/V blocks) one with the full register file.
 template <int DP, int DVP>
-constexpr int fused_waves_per_eu() { return DP > 128 || DVP > 128 ? 1 : 2; }
+constexpr int fused_waves_per_eu() { return DP > 128 || DVP > 128 ? 1 : (DP <= 64 && DVP <= 64 ? 3 : 2); }
 
 // P2: the scale is a power of two 2^k (-8 <= k <= 0), bf16 inputs, no additive mask.  Then
 // round(round(S) * scale) = round(S) * scale exactly whenever the product is a normal number (a
@@ -198,7 +200,8 @@ constexpr int fused_waves_per_eu() { return DP > 128 || DVP > 128 ? 1 : 2; }
 // exponentials: scale * log2(e) is exact too, and so are the products with it.  Only a product
 // below 2^-126 in magnitude (a bf16 denormal) skips its rounding.
 template <typename T, int DP, int DVP, int MASK, bool VARLEN, bool P2>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves_per_eu<DP, DVP>(), 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves_per_eu<DP, DVP>(),
+                                                                     fused_waves_per_eu<DP, DVP>() < 2 ? 2 : fused_waves_per_eu<DP, DVP>())))
 void fused_attn_kernel(FusedArgs a) {
   static_assert(!P2 || (MASK != 2 && std::is_same<T, bf16_t>::value), "power-of-two scale path");
   using F = FusedTile<T, DP, DVP>;
