@@ -71,8 +71,9 @@ constexpr int kBigAutoCount = kNumBig - 1;  // blocks the automatic choice weigh
 static const double kBigNmajorShare[kNumBig] = {0.93, 0.91, 0.87, 0.87, 0.88, 0.79, 0.86};
 constexpr int kBigEnd = kBigCfg + kNumBig;
 // Entries 20-22: the weight-streaming tile (gemm_stream.h), one m-tile of 16 (entry 20), 32
-// (entry 21) or 64 (entry 22) rows x 64 output columns per workgroup.  Grouped rows with a
-// 16-bit N-major B only (the MoE expert GEMMs); elsewhere they fall back to the automatic choice.
+// (entry 21) or 64 (entry 22) rows x 64 output columns per workgroup (128 for a plain
+// epilogue on 64-row m-tiles).  Grouped rows with a 16-bit N-major B only (the MoE
+// expert GEMMs); elsewhere they fall back to the automatic choice.
 constexpr int kStreamCfg = kBigEnd;
 constexpr int kNumStream = 3;
 constexpr int kStreamBM[kNumStream] = {16, 32, 64};
@@ -410,13 +411,13 @@ static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
   return launch_skinny_block<T, AR, 32>(a, stream);
 }
 
-// Grouped rows, 16-bit N-major B: one m-tile x 64 output columns per workgroup.  Like the
+// Grouped rows, 16-bit N-major B: one m-tile x 64 (WIDE: 128) output columns per workgroup.  Like the
 // one-tile-per-workgroup grouped entries, XCD x (workgroups g with g % 8 == x) takes the x-th
 // eighth of the tiles; the tiles are numbered column-block-major, so the m-tiles of one group
 // and column block (the same weights) fall on one XCD and its L2.
-template <typename T, int BM, bool SWIGLU>
-__global__ __launch_bounds__((StreamTile<T, BM, SWIGLU>::THREADS)) void stream_kernel(BmmArgs args) {
-  using S = StreamTile<T, BM, SWIGLU>;
+template <typename T, int BM, bool SWIGLU, bool WIDE>
+__global__ __launch_bounds__((StreamTile<T, BM, SWIGLU, WIDE>::THREADS)) void stream_kernel(BmmArgs args) {
+  using S = StreamTile<T, BM, SWIGLU, WIDE>;
   __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
   const uint32_t J = (uint32_t)args.grp[0];
   const uint32_t total = J * (uint32_t)args.tiles_n;
@@ -427,7 +428,7 @@ __global__ __launch_bounds__((StreamTile<T, BM, SWIGLU>::THREADS)) void stream_k
   const uint32_t tn = t / J, tm = t - tn * J;
   const int32_t* e = args.grp + kGrpHeader + kGrpStride * tm;
   const int64_t m0 = e[1], rows = e[2] - e[1];
-  const int64_t n0 = (int64_t)tn * S::OUT;
+  const int64_t n0 = (int64_t)tn * S::BLOCK_OUT;
   const int64_t boff = (int64_t)e[0] * args.sB1 + n0;
   typename S::Sources src;
   src.A = reinterpret_cast<const T*>(args.A);
@@ -436,7 +437,7 @@ __global__ __launch_bounds__((StreamTile<T, BM, SWIGLU>::THREADS)) void stream_k
   src.m0 = m0;
   src.rows = rows < BM ? (int)rows : BM;
   src.bg = reinterpret_cast<const T*>(args.B) + boff;
-  src.bu = reinterpret_cast<const T*>(SWIGLU ? args.B2 : args.B) + boff;
+  src.bu = reinterpret_cast<const T*>(SWIGLU ? args.B2 : args.B) + boff + (WIDE ? S::OUT : 0);
   src.ldb = args.ldb;
   src.ncols = args.N - n0;
   src.K = args.K;
@@ -446,15 +447,16 @@ __global__ __launch_bounds__((StreamTile<T, BM, SWIGLU>::THREADS)) void stream_k
 
 template <typename T, int BM, bool SWIGLU>
 static int launch_stream(const BmmArgs& a0, hipStream_t stream) {
+  constexpr bool WIDE = !SWIGLU && BM == 64;  // 128-column plain blocks
+  using S = StreamTile<T, BM, SWIGLU, WIDE>;
   BmmArgs a = a0;
   a.tiles_m = cdiv(a.grp_rows, BM) + std::min(a.grp_groups, a.grp_rows);
-  a.tiles_n = cdiv(a.N, StreamTile<T, BM, SWIGLU>::OUT);
+  a.tiles_n = cdiv(a.N, S::BLOCK_OUT);
   a.total = a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int64_t grid = (a.total + 7) & ~int64_t(7);
-  hipLaunchKernelGGL((stream_kernel<T, BM, SWIGLU>), dim3((unsigned)grid),
-                     dim3(StreamTile<T, BM, SWIGLU>::THREADS), 0, stream, a);
+  hipLaunchKernelGGL((stream_kernel<T, BM, SWIGLU, WIDE>), dim3((unsigned)grid), dim3(S::THREADS), 0, stream, a);
   return check_launch("stream_kernel");
 }
 

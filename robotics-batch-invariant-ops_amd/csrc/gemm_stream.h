@@ -13,7 +13,13 @@
 // Arithmetic: v_mfma_f32_16x16x32 on 16-row x 16-column blocks, quad q' of a 128-byte K step
 // feeding chunks 4q'..4q'+3 (the chain of the skinny entry, gemm_skinny.h, whose bits equal
 // those of the two 32x32x16 pair steps of every other entry), K in order, no split.  Plain:
-// four wavefronts, wavefront w owns output columns 16w..16w+15.  SwiGLU: eight wavefronts,
+// four wavefronts, wavefront w owns output columns 16w..16w+15.  Plain WIDE (the launcher
+// takes it for 64-row m-tiles): eight wavefronts over 128 output columns in two 64-column
+// halves, loaded and read as the SwiGLU mode's gate and up halves; half the workgroups, and
+// each A row read by half as many (MI355X, same-box A/B, same bits, per C5 MoE call: 256
+// tokens, the down GEMM on 64-row m-tiles, 155.0 -> 140.6 us, 4096 tokens (its tails)
+// 478.1 -> 469.4 us; with 32-row m-tiles it measured slower, 32 tokens 123.9 -> 127.1 us,
+// with 16-row ones even at one to four tokens).  SwiGLU: eight wavefronts,
 // wavefront w owns the gate (w < 4) or up (w >= 4) columns 16(w%4)..+15, which halves each
 // wavefront's work per stage (one-token gate/up GEMM of 8 experts: 14.7 -> 11.8 us); after the
 // K loop the up wavefronts pass their accumulators through LDS to the gate wavefront of the
@@ -35,13 +41,16 @@
 
 namespace biops {
 
-template <typename T, int BM, bool SWIGLU>
+template <typename T, int BM, bool SWIGLU, bool WIDE = false>
 struct StreamTile {
   static_assert(sizeof(T) == 2, "16-bit operands");
   static_assert(BM == 16 || BM == 32 || BM == 64, "m-tile rows");
-  static constexpr int THREADS = SWIGLU ? 512 : 256;
-  static constexpr int OUT = 64;                          // output columns of a block
-  static constexpr int CPR = (SWIGLU ? 2 : 1) * OUT / 8;  // 16-byte chunks of a B K row (8 / 16)
+  static_assert(!(SWIGLU && WIDE), "one mode");
+  static constexpr bool TWO = SWIGLU || WIDE;             // two 64-column halves of B per block
+  static constexpr int THREADS = TWO ? 512 : 256;
+  static constexpr int OUT = 64;                          // output columns of a half
+  static constexpr int BLOCK_OUT = WIDE ? 2 * OUT : OUT;  // output columns of a block
+  static constexpr int CPR = (TWO ? 2 : 1) * OUT / 8;     // 16-byte chunks of a B K row (8 / 16)
   static constexpr int SK = 128;                          // K elements of a stage
   static constexpr int STEPS = SK / 64;                   // 128-byte K steps of a stage
   static constexpr int RB = BM / 16;                      // 16-row MFMA blocks
@@ -58,8 +67,8 @@ struct StreamTile {
   // one-row groups, K = 768, took 48.5 us with an 8-stage ring and 31.0 us with 4, of 8 groups
   // 6.4 and 5.6 us, MI355X); with 64-row m-tiles, whose stages are twice as large, 4 stages in
   // 160 KiB.
-  static constexpr int STAGES_FIT = (SWIGLU || BM == 64 ? 160 * 1024 : 80 * 1024) / LDS_STAGE;
-  static constexpr int STAGES = STAGES_FIT < (SWIGLU ? 8 : 4) ? STAGES_FIT : (SWIGLU ? 8 : 4);
+  static constexpr int STAGES_FIT = (TWO || BM == 64 ? 160 * 1024 : 80 * 1024) / LDS_STAGE;
+  static constexpr int STAGES = STAGES_FIT < (TWO ? 8 : 4) ? STAGES_FIT : (TWO ? 8 : 4);
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
   static constexpr int A_LOADS = A_SLOTS < THREADS ? 1 : A_SLOTS / THREADS;  // per thread and stage
   static constexpr int B_LOADS = SK * CPR / THREADS;
@@ -149,10 +158,19 @@ struct StreamTile {
       const int s = t + THREADS * p;
       const int k = s / CPR;
       const int c = (s % CPR) ^ bswz(k);
-      const bool up = SWIGLU && c >= 8;
-      int64_t col = (int64_t)(up ? c - 8 : c) * 8;
-      if (col + 8 > S.ncols) col = S.ncols - 8;
-      bsrc[p] = (up ? S.bu : S.bg) + col;
+      const bool hi = TWO && c >= 8;
+      const T* base = hi ? S.bu : S.bg;
+      int64_t nc = S.ncols;
+      if (WIDE && hi) {
+        nc = S.ncols - OUT;  // the upper half's valid columns
+        if (nc < 8) {        // none: any whole chunk of the lower half (never stored)
+          base = S.bg;
+          nc = S.ncols;
+        }
+      }
+      int64_t col = (int64_t)(hi ? c - 8 : c) * 8;
+      if (col + 8 > nc) col = nc - 8;
+      bsrc[p] = base + col;
       brow[p] = k;
     }
     auto issue = [&](int64_t st) {
@@ -177,7 +195,7 @@ struct StreamTile {
     const int lane = t & 63, w = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     // Output column block jb of this wavefront, and the B part it reads (SwiGLU: 0 gate, 1 up).
-    const int jb = SWIGLU ? (w & 3) : w, part = SWIGLU ? (w >> 2) : 0;
+    const int jb = TWO ? (w & 3) : w, part = TWO ? (w >> 2) : 0;
     // Transposing reads: source lane lr points at K row 8 lg + lr / 4 (+ 4 for the upper half),
     // column 4 (lr % 4) of the wavefront's 16-column block.
     const int tr_k = 8 * lg + (lr >> 2), tr_c = OUT * part + 16 * jb + 4 * (lr & 3);
@@ -249,7 +267,7 @@ struct StreamTile {
   __device__ static __forceinline__ void store(const Acc& acc, T* C, int64_t ldc, int rows, int64_t cols) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (SWIGLU && w >= 4) return;
-    const int col = 16 * (w & 3) + (lane & 15);
+    const int col = (WIDE ? OUT * (w >> 2) : 0) + 16 * (w & 3) + (lane & 15);
     if (col >= cols) return;
 #pragma unroll
     for (int i = 0; i < RB; ++i)
