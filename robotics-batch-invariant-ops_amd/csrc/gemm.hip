@@ -374,14 +374,15 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // against 11.4).
   if ((best == 4 || best == 6) && prefer32) best = (big_ok && !nmajor16) ? kBigCfg + 6 : 6;
   if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
-  // Grouped rows of at most 40 rows per group on average with a 16-bit N-major B (the MoE
-  // expert GEMMs of calls up to about 5E/k tokens): the weight-streaming entries.  MI355X, C5
+  // Grouped rows of at most 56 rows per group on average with a 16-bit N-major B (the MoE
+  // expert GEMMs of calls up to about 7E/k tokens): the weight-streaming entries.  MI355X, C5
   // shapes (E = 64, D = 2048, I = 768, top-8), per sparse MoE call against the best table entry:
   // 1 token 47.1 us (16 rows) against 62.8 (entry 7); 2 tokens 56.3 against 74.5 (entry 2);
   // 32 tokens 154.6 (32 rows) against 171.4; 128 tokens 130.5 (32 rows) against 160.9; 256
-  // tokens (32 rows per group) 160.1 (64 rows) against 170.8; at 384 tokens entry 2 wins,
-  // 175.2 against 182.3 (64 rows).
-  if (stream_ok && mean <= 40)
+  // tokens (32 rows per group) 160.1 (64 rows) against 170.8.  With the 128-column plain
+  // blocks of 64-row m-tiles (same box): 384 tokens 167.3-173.0 against 173.8 (entry 2), 448
+  // tokens 170.5 against 176.3; at 512 tokens entry 2 wins, 176.7 against 184.7.
+  if (stream_ok && mean <= 56)
     best = mean <= 2 ? kStreamCfg : mean <= 16 ? kStreamCfg + 1 : kStreamCfg + 2;
   return best;
 }
