@@ -106,7 +106,8 @@ struct StreamTile {
   };
 
   // Operand sources of one block.  a_row(r): A row of m-tile row r (r < rows); B: gate / plain
-  // columns at bg + n, up columns at bu + n (N-major, K row k at + k * ldb), n < ncols.
+  // columns at bg + n, up columns at bu + n (N-major, K row k at + k * ldb), n < ncols; WIDE:
+  // the block's columns OUT + n at bu + n (bu = bg + OUT), valid for n < ncols - OUT.
   struct Sources {
     const T* A;
     int64_t lda;
