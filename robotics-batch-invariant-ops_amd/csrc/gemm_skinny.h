@@ -3,13 +3,15 @@
 //
 // One workgroup owns one 32 x BC output block (BC = 32, 16 or 8 columns).  Wavefront 0
 // computes it over K steps of 128 bytes in order, with the arithmetic of SkinnyMath below
-// (bits equal to those of every other tile entry).  What differs is how operands arrive: eight wavefronts share the 1 KiB
-// global->LDS load instructions of a stage (8 K steps, 1 KiB of every row) round-robin, into a
-// ring of 2-4 stages (up to the 160 KiB of a compute unit), and one barrier per stage publishes
-// it.  On MI355X a compute unit's load rate grows with the bytes per row per stage and with the
-// number of issuing wavefronts (4 KiB per-step stages on one wavefront: ~37 GB/s; 8-step
-// stages on 8 wavefronts: ~2x).  With few rows a block's time is the serial K chain of its
-// accumulator and the bytes it streams; the ring keeps the stream ahead of the chain.
+// (bits equal to those of every other tile entry).  What differs is how operands arrive: eight
+// wavefronts share the 1 KiB global->LDS load instructions of a stage (4 or 8 K steps, 512 or
+// 1024 bytes of every row) round-robin, into a ring of 2-4 stages (up to the 160 KiB of a
+// compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate
+// grows with the bytes per row per stage and with the number of issuing wavefronts (4 KiB
+// per-step stages on one wavefront: ~37 GB/s; 8-step stages on 8 wavefronts: ~2x), but not
+// with the bytes in flight past a few stages.  With few rows a block's time is the serial K
+// chain of its accumulator and the bytes it streams; the ring keeps the stream ahead of the
+// chain.
 //
 // Only AR A rows are loaded (AR = 8, 16 or 32, the rows a block can hold); MFMA rows past AR
 // read loaded rows again (row r reads row r mod AR) and, like rows past M, are never stored.
@@ -162,14 +164,21 @@ struct SkinnyTile {
   static constexpr int IPK = AR / 8 + BC / 8;             // 1 KiB load instructions per K step
   static constexpr int LDS_A = AR * kKBytes;             // A rows of one K step
   static constexpr int LDS_KSTEP = LDS_A + BC * kKBytes;  // one K step: A rows, then B columns
-  static constexpr int U = 8;                             // K steps per stage (even)
+  // K steps per stage: 4 for the blocks of at least 48 rows + columns whose 4-step stage deals
+  // evenly over the wavefronts (32 x 32, 32 x 16, 16 x 32), 8 for the others.  Ring: as deep as
+  // 160 KiB allows, at most 4 stages, 2 for 8 x 32 blocks.  Fewer bytes in flight measured
+  // faster on MI355X (bf16, same-box A/B in alternating order, same bits): M = 64, N = 2048,
+  // K = 8192 (32 x 16) 15.0 -> 12.6 us with 4-step stages (4 of 24 KiB instead of 3 of 48);
+  // M = 16 / 32, N = 8192, K = 2048 (16 x 32 / 32 x 32) 7.6 -> 6.6 / 9.3 -> 8.8 us; one to eight
+  // rows, N = 8192, K = 2048 (8 x 32) 6.7-7.1 -> 6.4-6.8 us with 2 stages instead of 4; 3, 6 and
+  // 8 stages were slower, and so were deeper rings of the narrow blocks (N = 2048, K = 8192,
+  // one row, 8-column blocks: 13.8 us at 8 stages, 13.3 us at 4, against 12.5 us for the bare
+  // chain of 512 dependent MFMAs).
+  static constexpr int U = (IPK * 4) % WAVES == 0 && AR + BC >= 48 ? 4 : 8;
   static constexpr int LDS_STAGE = U * LDS_KSTEP;
-  // as deep as 160 KiB allows (4 / 3 / 2 for AR = 8 / 16 / 32 at BC = 32), at most 4 stages:
-  // deeper rings of the narrow blocks measured slower (N = 2048, K = 8192, one row, 8-column
-  // blocks: 13.8 us at 8 stages, 13.3 us at 4, against 12.5 us for the bare chain of 512
-  // dependent MFMAs)
+  static constexpr int MAX_STAGES = AR == 8 && BC == 32 ? 2 : 4;
   static constexpr int STAGES_FIT = (160 * 1024) / LDS_STAGE;
-  static constexpr int STAGES = STAGES_FIT < 4 ? STAGES_FIT : 4;
+  static constexpr int STAGES = STAGES_FIT < MAX_STAGES ? STAGES_FIT : MAX_STAGES;
   static constexpr int LDS_BYTES = STAGES * LDS_STAGE;
   static constexpr int LOADS = U * IPK / WAVES;           // per wavefront per stage
   static_assert(U * IPK % WAVES == 0, "uniform loads per wavefront");
