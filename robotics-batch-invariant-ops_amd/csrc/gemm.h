@@ -39,6 +39,7 @@ struct BmmArgs {
   // filled by the launcher
   int64_t tiles_m, tiles_n, total;
   int32_t a_vec, b_vec, c_vec;
+  int32_t nt_store;  // four-wave entries: whole tiles store with non-temporal stores
 };
 
 constexpr int kGrpHeader = 4;

@@ -260,7 +260,7 @@ void big_kernel(BmmArgs args) {
   Tile::mainloop(smem, acc, A, args.lda, rows, B, args.ldb, cols, args.K);
   T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0;
   const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + o.n0 : nullptr;
-  Tile::epilogue(acc, Cp, args.ldc, rows, cols, bias);
+  Tile::epilogue(acc, Cp, args.ldc, rows, cols, bias, args.nt_store != 0);
 }
 
 // -------------------------------------------------------------- tile selection ----
@@ -469,6 +469,9 @@ static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
   if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  const int cus = device_cus();
+  if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
+  a.nt_store = a.total <= cus ? 1 : 0;  // one round: non-temporal output stores (gemm_big.h)
   hipLaunchKernelGGL((big_kernel<T, BM, BN, SB, BKM>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
   return check_launch("big_kernel");
 }

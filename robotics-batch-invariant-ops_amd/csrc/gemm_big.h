@@ -394,7 +394,9 @@ struct BigTile {
   // requires BM * ldc < 2^31); the opaque copy of ldc keeps the compiler from holding all
   // row offsets in registers.  A whole tile stores without per-value bounds checks: the 256
   // branches of the checked form cost 6-8 us per launch at M = 4096, N = 8192 (MI355X).
-  template <bool CHECKED>
+  // NT: non-temporal stores (whole tiles of a launch that fills one round of the compute units;
+  // see epilogue()).
+  template <bool CHECKED, bool NT = false>
   __device__ static __forceinline__ void store_tile(Acc (&acc)[FM][FN], T* C, int ldc32, int rows, int cols,
                                                     const T* bias) {
 #pragma unroll
@@ -407,19 +409,34 @@ struct BigTile {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = acc_row(i, r);
-          if (!CHECKED || (col_ok && row < rows))
-            Num<T>::store(C + (uint32_t)(row * ldc32 + col), bias ? acc[i][j][r] + bv : acc[i][j][r]);
+          if (!CHECKED || (col_ok && row < rows)) {
+            const float v = bias ? acc[i][j][r] + bv : acc[i][j][r];
+            T* p = C + (uint32_t)(row * ldc32 + col);
+            if constexpr (NT)
+              __builtin_nontemporal_store(Num<T>::to_bits(v), reinterpret_cast<uint16_t*>(p));
+            else
+              Num<T>::store(p, v);
+          }
         }
       }
   }
+  // With `nt` (set by the launcher when the launch's tiles fit one round of the compute units)
+  // whole tiles store non-temporally.  Measured on MI355X (bf16, same-box A/B, same bits):
+  // one-round launches 512 / 1024 / 2048 x 8192 x 2048 25.2 -> 23.9, 39.3 -> 37.3,
+  // 62.6 -> 60.8 us and 2048 x 2048 x 8192 70.2 -> 68.9 us; launches of several rounds slower
+  // (4096 x 8192 x 2048 120.2 -> 126.9 us), so they keep ordinary stores.
   __device__ static __forceinline__ void epilogue(Acc (&acc)[FM][FN], T* C, int64_t ldc, int rows, int cols,
-                                                  const T* bias) {
+                                                  const T* bias, bool nt) {
     int ldc32 = (int)ldc;
     asm volatile("" : "+s"(ldc32));
-    if (rows == BM && cols == BN)
-      store_tile<false>(acc, C, ldc32, rows, cols, bias);
-    else
+    if (rows == BM && cols == BN) {
+      if (nt)
+        store_tile<false, true>(acc, C, ldc32, rows, cols, bias);
+      else
+        store_tile<false>(acc, C, ldc32, rows, cols, bias);
+    } else {
       store_tile<true>(acc, C, ldc32, rows, cols, bias);
+    }
   }
 };
 
