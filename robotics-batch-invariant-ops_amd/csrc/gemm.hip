@@ -42,7 +42,7 @@ BIOPS_CFG(10, 256, 128, 4, 2, 3, 1, false, 0)
 BIOPS_CFG(11, 128, 256, 2, 4, 3, 1, false, 0)
 #undef BIOPS_CFG
 constexpr int kNumCfg = 12;
-// Entry 12: the skinny tile (gemm_skinny.h), one 32-row block (32, 16 or 8 columns) per
+// Entry 12: the skinny tile (gemm_skinny.h), one 32-row block (64, 32, 16 or 8 columns) per
 // workgroup with loader wavefronts.  Needs the direct-load conditions and a plain / bias epilogue; elsewhere it falls
 // back to the automatic choice.
 constexpr int kSkinnyCfg = kNumCfg;
@@ -235,10 +235,12 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   const int rows = rows64 < 32 ? (int)rows64 : 32;
   const int cols = cols64 < BC ? (int)cols64 : BC;
   const typename S::Acc acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
-  if ((threadIdx.x >> 6) != 0) return;
-  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + o.n0;
-  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + o.n0 : nullptr;
-  S::Math::store(acc, Cp, args.ldc, rows, cols, bias);
+  const int w = threadIdx.x >> 6;  // computing wavefront w stores columns 32w .. 32w+31
+  if (w >= S::CW) return;
+  const int64_t n0 = o.n0 + 32 * w;
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + n0;
+  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
+  S::Math::store(acc, Cp, args.ldc, rows, cols - 32 * w, bias);
 }
 
 template <typename T, int BM, int BN, int SB, bool BKM>
@@ -373,7 +375,16 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // M = 256: 33.3 against 34.5; M = 128, N = 8192, K = 2048: 11.6 against 12.4; M = 64: 10.9
   // against 11.4).
   if ((best == 4 || best == 6) && prefer32) best = (big_ok && !nmajor16) ? kBigCfg + 6 : 6;
-  if (skinny_ok && batch * cdiv(a.M, 32) * cdiv(a.N, 32) <= cus) best = kSkinnyCfg;
+  // The skinny entry: 32-column (or narrower) blocks in one round, or, with at least two row
+  // blocks and K >= 1024, 64-column blocks in one round (MI355X, bf16, same-box A/B against the
+  // automatic choice before them, same bits: 256 x 2048 x 8192 33.7 -> 26.8 us, 128 x 4096 x
+  // 4096 18.3 -> 15.6 us, 512 x 1024 x 4096 18.3 -> 15.5 us, 96 x 5000 x 2048 11.6 -> 10.1 us,
+  // 512 x 1024 x 1024 7.9 -> 7.3 us; with one row block or K = 512 they lost: 32 x 16384 x
+  // 2048 13.0 -> 14.0 us, 64 x 8192 x 512 6.0 -> 6.3 us).
+  const int64_t row_blocks = batch * cdiv(a.M, 32);
+  if (skinny_ok && (row_blocks * cdiv(a.N, 32) <= cus ||
+                    (row_blocks >= 2 && a.K >= 1024 && row_blocks * cdiv(a.N, 64) <= cus)))
+    best = kSkinnyCfg;
   // Grouped rows of at most 56 rows per group on average with a 16-bit N-major B (the MoE
   // expert GEMMs of calls up to about 7E/k tokens): the weight-streaming entries.  MI355X, C5
   // shapes (E = 64, D = 2048, I = 768, top-8), per sparse MoE call against the best table entry:
@@ -394,22 +405,27 @@ static int launch_skinny_block(const BmmArgs& a0, hipStream_t stream) {
   a.tiles_n = cdiv(a.N, BC);
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
-  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
-  hipLaunchKernelGGL((skinny_kernel<T, AR, BC>), dim3((unsigned)a.total),
+  if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  // a whole number of workgroups per XCD, so that xcd_slot keeps neighbouring blocks (which
+  // share A rows and B columns) on one XCD; the extra workgroups exit at once
+  const int64_t grid = (a.total + 7) & ~int64_t(7);
+  hipLaunchKernelGGL((skinny_kernel<T, AR, BC>), dim3((unsigned)grid),
                      dim3(SkinnyTile<T, AR, BC>::THREADS), 0, stream, a);
   return check_launch("skinny_kernel");
 }
 
-// Block width: the narrowest of 32 / 16 / 8 columns whose blocks still fit one round on the
-// compute units (N = 2048: 8 columns at M <= 32, 16 columns at M = 64).  Measured on MI355X,
-// N = 2048, K = 8192: M = 64 takes 15.5 us at 16 columns against 19.8 us at 32.
+// Block width: the narrowest of 8 / 16 / 32 / 64 columns whose blocks still fit one round on the
+// compute units (N = 2048: 8 columns at M <= 32, 16 columns at M = 64, 64 columns at M = 256).
+// Measured on MI355X, N = 2048, K = 8192: M = 64 takes 15.5 us at 16 columns against 19.8 us
+// at 32.
 template <typename T, int AR>
 static int launch_skinny_rows(const BmmArgs& a, hipStream_t stream) {
   const int64_t cus = device_cus();
   const int64_t row_blocks = a.nb1 * a.nb2 * cdiv(a.M, 32);
   if (row_blocks * cdiv(a.N, 8) <= cus) return launch_skinny_block<T, AR, 8>(a, stream);
   if (row_blocks * cdiv(a.N, 16) <= cus) return launch_skinny_block<T, AR, 16>(a, stream);
-  return launch_skinny_block<T, AR, 32>(a, stream);
+  if (row_blocks * cdiv(a.N, 32) <= cus) return launch_skinny_block<T, AR, 32>(a, stream);
+  return launch_skinny_block<T, AR, 64>(a, stream);
 }
 
 // Grouped rows, 16-bit N-major B: one m-tile x 64 (WIDE: 128) output columns per workgroup.  Like the
@@ -468,11 +484,12 @@ static int launch_big(const BmmArgs& a0, hipStream_t stream) {
   a.tiles_n = cdiv(a.N, BN);
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
-  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int cus = device_cus();
   if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
   a.nt_store = a.total <= cus ? 1 : 0;  // one round: non-temporal output stores (gemm_big.h)
-  hipLaunchKernelGGL((big_kernel<T, BM, BN, SB, BKM>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
+  const int64_t grid = (a.total + 7) & ~int64_t(7);  // whole workgroups per XCD (xcd_slot)
+  hipLaunchKernelGGL((big_kernel<T, BM, BN, SB, BKM>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return check_launch("big_kernel");
 }
 

@@ -1,9 +1,9 @@
 // Skinny GEMM tile for problems with few rows (decode-size linears): one 32 x BC block per
 // workgroup, used when all blocks of a launch fit one round on the compute units.
 //
-// One workgroup owns one 32 x BC output block (BC = 32, 16 or 8 columns).  Wavefront 0
-// computes it over K steps of 128 bytes in order, with the arithmetic of SkinnyMath below
-// (bits equal to those of every other tile entry).  What differs is how operands arrive: eight
+// One workgroup owns one 32 x BC output block (BC = 64, 32, 16 or 8 columns).  Wavefront 0
+// (wavefronts 0 and 1 for 64 columns, 32 each) computes it over K steps of 128 bytes in order,
+// with the arithmetic of SkinnyMath below (bits equal to those of every other tile entry).  What differs is how operands arrive: eight
 // wavefronts share the 1 KiB global->LDS load instructions of a stage (4 or 8 K steps, 512 or
 // 1024 bytes of every row) round-robin, into a ring of 2-4 stages (up to the 160 KiB of a
 // compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate
@@ -156,8 +156,11 @@ struct SkinnyMath<T, AR, BC, false> {
 template <typename T, int AR, int BC>
 struct SkinnyTile {
   static_assert(AR == 8 || AR == 16 || AR == 32, "A rows per K step");
-  static_assert(BC == 8 || BC == 16 || BC == 32, "B columns per K step");
+  static_assert(BC == 8 || BC == 16 || BC == 32 || BC == 64, "B columns per K step");
   static constexpr int WAVES = 8;
+  // Wavefronts that compute: one per 32 columns of the block (a 64-column block splits its
+  // MFMA chains over two); all eight load.
+  static constexpr int CW = BC > 32 ? BC / 32 : 1;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
@@ -201,7 +204,12 @@ struct SkinnyTile {
   using Math = SkinnyMath<T, AR, BC>;
   using Acc = typename Math::Acc;
   using Frags = typename Math::Frags;
-  __device__ static __forceinline__ void load_frags(const char* kstep, Frags& f) { Math::load(kstep, LDS_A, f); }
+  // Computing wavefront w reads columns 32w .. 32w+31 (the lds_off swizzle of a column only
+  // depends on its index modulo 16).
+  __device__ static __forceinline__ void load_frags(const char* kstep, Frags& f) {
+    const int bofs = CW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 32 * kKBytes : 0;
+    Math::load(kstep, LDS_A + bofs, f);
+  }
   __device__ static __forceinline__ void mfma(Acc& acc, const Frags& f) {
 #pragma unroll
     for (int n = 0; n < Math::COUNT; ++n) Math::one(acc, f, n);
@@ -230,9 +238,9 @@ struct SkinnyTile {
   // The 32 x BC block at (A, B) with `rows` / `cols` valid rows and columns (>= 1) over KT K
   // steps.  Stage s holds K steps s*U .. s*U+U-1 (the last stage may hold fewer).  The U*IPK
   // 1 KiB load instructions of a stage (K step u, part p: A rows 8p..8p+7 or B columns) are
-  // dealt round-robin to the 8 wavefronts.  Returns the accumulator in wavefront 0 (other
-  // wavefronts return zeros once their last load is issued; the kernel only lets wavefront 0
-  // continue).
+  // dealt round-robin to the 8 wavefronts.  Returns the accumulator of columns 32w .. 32w+31
+  // in computing wavefront w < CW (the other wavefronts return zeros once their last load is
+  // issued; the kernel only lets the computing wavefronts continue).
   __device__ static __forceinline__ Acc run(char* smem, const T* A, int64_t lda, int rows,
                                             const T* B, int64_t ldb, int cols, int64_t KT) {
     Acc acc;
@@ -277,9 +285,9 @@ struct SkinnyTile {
     wait_loads<(STAGES - 1) * LOADS>();  // stage 0 landed
     lds_barrier();
     // Stages 0 .. NS-2 are full (U steps) and each ends with the barrier that publishes the next
-    // stage; the last stage (1..U steps) has none.  Wavefront 0 and the loader wavefronts run
+    // stage; the last stage (1..U steps) has none.  The computing and the loader wavefronts run
     // separate branch-free loops that meet at the same barriers.
-    if (w != 0) {
+    if (w >= CW) {
       for (int64_t s = 0; s + 1 < NS; ++s) {
         wait_loads<(STAGES - 2) * LOADS>();  // stage s+1 landed
         lds_barrier();

@@ -336,6 +336,32 @@ def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+@pytest.mark.parametrize(("m", "n", "k"), (
+    (256, 2048, 2048),   # 8 row blocks x 32 blocks of 64 columns: one round
+    (64, 8100, 1024),    # 2 x 127 blocks, 36-column last block (wavefront 1 stores 4 columns)
+    (256, 2000, 1024),   # 16-column last block: wavefront 1 of that block stores nothing
+    (33, 16384, 1024),   # 2 x 256 blocks: more than one round, forced
+))
+def test_skinny_64_column_blocks_give_identical_bits(tile_menu, dtype, m, n, k):
+    """With at least two row blocks the skinny entry also takes 64-column blocks, split over two
+    computing wavefronts of 32 columns each; rows keep the bits of entry 2, with and without a
+    bias, and of a call on the last row alone.  The automatic choice takes them where they fit
+    one round."""
+    x = gpu(randn(m, k, seed=5500 + m, dtype=dtype))
+    w = gpu(randn(n, k, seed=5501 + n, dtype=dtype) * 0.05)
+    bias = gpu(randn(n, seed=5502, dtype=dtype))
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = matmul_persistent(x, w.t(), bias)
+    ref_plain = matmul_persistent(x, w.t())
+    assert tile_menu.biops_set_gemm_tile(SKINNY_ENTRY) == 0
+    assert_bitwise(matmul_persistent(x, w.t(), bias), ref, "skinny entry")
+    assert_bitwise(matmul_persistent(x, w.t()), ref_plain, "skinny entry, no bias")
+    assert_bitwise(matmul_persistent(x[m - 1:], w.t(), bias), ref[m - 1:], "skinny entry, last row")
+    assert tile_menu.biops_set_gemm_tile(-1) == 0
+    assert_bitwise(matmul_persistent(x, w.t(), bias), ref, "automatic choice")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 @pytest.mark.parametrize(("m", "k", "n"), (
     (300, 2048, 520),   # N-major direct loads, partial last column tile
     (77, 1024, 256),
