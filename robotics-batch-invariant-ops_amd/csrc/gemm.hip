@@ -511,12 +511,14 @@ static int launch_cfg(const BmmArgs& a0, hipStream_t stream) {
   a.tiles_n = cdiv(a.N, kCols);
   a.total = (grouped ? 1 : a.nb1 * a.nb2) * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
-  if (a.total >= (int64_t(1) << 31)) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
+  if (a.total >= (int64_t(1) << 31) - 8) return fail(BIOPS_ERR_SIZE, "too many GEMM tiles");
   const int cus = device_cus();
   if (cus <= 0) return fail(BIOPS_ERR_HIP, "no HIP device");
   int64_t grid = C::persist ? (int64_t)cus * C::per_cu : a.total;
   if (a.total < grid) grid = a.total;
-  if (grouped) grid = (grid + 7) & ~int64_t(7);
+  // whole workgroups per XCD: the grouped walk deals tiles by XCD, and xcd_slot keeps
+  // neighbouring tiles on one XCD only then; the extra workgroups find no tile
+  grid = (grid + 7) & ~int64_t(7);
   hipLaunchKernelGGL((bmm_kernel<T, CFG, BKM, DIRECT, EPI, GRP>), dim3((unsigned)grid), dim3(C::threads),
                      0, stream, a);
   return check_launch("bmm_kernel");
