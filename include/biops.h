@@ -96,6 +96,33 @@ int biops_bmm(int dtype, int64_t nb1, int64_t nb2, int64_t M, int64_t N, int64_t
               void* C, int64_t sC1, int64_t sC2, int64_t sCm, int64_t sCn,
               void* stream);
 
+/* dst[rows_out, cols_out] (row pitch cols_out) = src[rows, cols] (row pitch ld_src, unit
+ * stride along a row), zero where r >= rows or c >= cols; rows_out >= rows, cols_out >= cols,
+ * cols_out * element size a multiple of 16 bytes, dst 16-byte aligned.  Operand staging for
+ * GEMMs whose K is not a whole number of 128-byte steps or whose rows are not 16-byte aligned:
+ * zero-padding K changes no product bit (out-of-range K is zero in both operands on every load
+ * path), and the padded operands take the direct global->LDS loads.  No counterpart in the
+ * reference, whose masked Triton loads need no such copy. */
+int biops_pad_rows(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src,
+                   int64_t rows_out, int64_t cols_out, void* dst, void* stream);
+
+/* Workspace bytes biops_gemm_padded needs for an M x N x K product whose B has strides
+ * (sBk, sBn); -1 for an unsupported dtype or layout.  No counterpart in the reference. */
+int64_t biops_gemm_padded_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t sBk, int64_t sBn);
+
+/* biops_gemm (same arguments and bits) on zero-padded copies of A and B written into
+ * `workspace` (256-byte aligned, biops_gemm_padded_workspace_size bytes): K rounded up to a
+ * whole number of 128-byte steps, rows 16-byte aligned, so that every tile entry loads the
+ * operands straight into LDS.  For products whose K is not such a multiple or whose rows are
+ * misaligned and which are large enough to repay two copies.  No counterpart in the reference. */
+int biops_gemm_padded(int dtype, int64_t M, int64_t N, int64_t K,
+                      const void* A, int64_t sAm, int64_t sAk,
+                      const void* B, int64_t sBk, int64_t sBn,
+                      const void* bias,
+                      void* C, int64_t sCm, int64_t sCn,
+                      void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
 /* Number of entries in the GEMM tile menu.  Each entry is a (block tile, wavefront layout, LDS
  * ring depth) scheduling choice; all entries compute every output element with the same MFMA
  * sequence, so they produce identical bits and differ in speed only.  No reference

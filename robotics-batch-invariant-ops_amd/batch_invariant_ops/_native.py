@@ -46,6 +46,9 @@ _SIGNATURES = {
         _i,
         [_i, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p],
     ),
+    "biops_pad_rows": (_i, [_i, _l, _l, _p, _l, _l, _l, _p, _p]),
+    "biops_gemm_padded_workspace_size": (_l, [_i, _l, _l, _l, _l, _l]),
+    "biops_gemm_padded": (_i, [_i, _l, _l, _l, _p, _l, _l, _p, _l, _l, _p, _p, _l, _l, _p, _l, _p]),
     "biops_gemm_tile_count": (_i, []),
     "biops_set_gemm_tile": (_i, [_i]),
     "biops_softmax": (_i, [_i, _i, _l, _l, _p, _l, _p, _l, _i, _p]),
@@ -179,7 +182,7 @@ def function(name: str):
 
 # Entry points with a CPython fast-call binding (_biops_fast, built beside libbiops.so): the
 # same C functions and arguments, without ctypes' per-argument conversions.
-_FAST = {"biops_gemm": "gemm", "biops_reduce": "reduce", "biops_softmax": "softmax",
+_FAST = {"biops_gemm": "gemm", "biops_gemm_padded": "gemm_padded", "biops_reduce": "reduce", "biops_softmax": "softmax",
          "biops_sdpa_fused": "sdpa_fused", "biops_varlen_plan": "varlen_plan", "biops_varlen_fused_order": "varlen_fused_order",
          "biops_varlen_sdpa_fused": "varlen_sdpa_fused",
          "biops_varlen_sdpa_fused_planned": "varlen_sdpa_fused_planned"}

@@ -90,6 +90,42 @@ def _b_operand(b: torch.Tensor) -> torch.Tensor:
     return b.contiguous()
 
 
+# Products whose operands cannot take the direct global->LDS loads (K not a whole number of
+# 128-byte steps, or rows not 16-byte aligned) run through biops_gemm_padded, on zero-padded
+# copies, when they have at least this many multiply-adds and either misaligned rows (element
+# by element register loads) or rows of at least _PAD_MIN_K_BYTES; the others keep the register
+# load path of biops_gemm.  Both give the same bits: out-of-range K is zero in both operands on
+# every load path.  MI355X, bf16, per linear call (register path -> padded): 2048 x 2048 x 2050
+# 357 -> 42 us, 512 x 512 x 500 50 -> 26 us, 300 x 700 x 5000 77 -> 28 us, 1 x 4096 x 4000
+# 57 -> 27 us; with K = 1000 the register path was as fast or faster (256 x 1024 x 1000
+# 18 against 26 us).
+_PAD_MIN_WORK = 1 << 23
+_PAD_MIN_K_BYTES = 4000
+
+
+def _aligned16(t: torch.Tensor, ld: int) -> bool:
+    return t.data_ptr() % 16 == 0 and (ld * t.element_size()) % 16 == 0
+
+
+def _padded_workspace(a: torch.Tensor, b: torch.Tensor, M: int, N: int, K: int) -> int:
+    """Workspace bytes of biops_gemm_padded for A [M, K] and B [K, N] (unit stride in K or N),
+    or 0 when the product should call biops_gemm on the operands as they are."""
+    elt = a.element_size()
+    step = 128 // elt
+    kmajor = b.stride(0) == 1 or K <= 1
+    if not kmajor and b.stride(1) != 1 and N > 1:
+        return 0
+    ldb = b.stride(1) if kmajor else b.stride(0)
+    aligned = _aligned16(a, a.stride(0)) and _aligned16(b, ldb) and (kmajor or (N * elt) % 16 == 0)
+    if aligned and K % step == 0:
+        return 0
+    if M * N * K < _PAD_MIN_WORK or (aligned and K * elt < _PAD_MIN_K_BYTES):
+        return 0
+    kp = -(-K // step) * step
+    np_ = N if kmajor else -(-N * elt // 16) * 16 // elt
+    return -(-M * kp * elt // 256) * 256 + (N * kp if kmajor else kp * np_) * elt
+
+
 def matmul_persistent(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = None):
     """C = A @ B (+ bias) with a fixed tile, K order and MFMA instruction, fp32 accumulation.
 
@@ -117,6 +153,16 @@ def matmul_persistent(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | Non
         assert bias.shape[0] == N, "bias length must equal the number of output columns"
         bias = bias.to(a.dtype).contiguous()
         bias_ptr = bias.data_ptr()
+    stream = nat.stream_of(c)
+    ws_bytes = _padded_workspace(a, b, M, N, K) if K > 0 else 0
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, device=a.device, dtype=torch.uint8)
+        if ws.data_ptr() % 256 == 0:
+            rc = _fast_fn("biops_gemm_padded")(
+                code, M, N, K, a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1),
+                bias_ptr, c.data_ptr(), c.stride(0), c.stride(1), ws.data_ptr(), ws_bytes, stream)
+            nat.check(rc, "biops_gemm_padded")
+            return c
     nat.call(
         "biops_gemm",
         code, M, N, K,
@@ -124,7 +170,7 @@ def matmul_persistent(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | Non
         b.data_ptr(), b.stride(0), b.stride(1),
         bias_ptr,
         c.data_ptr(), c.stride(0), c.stride(1),
-        nat.stream_of(c),
+        stream,
     )
     return c
 
@@ -195,6 +241,15 @@ def _linear_direct(input, weight, bias):
     shape = input.shape
     if shape[-1] != k or k == 0 or n == 0:
         return None
+    elt = input.element_size()
+    if (k * elt) % 128:
+        # K not a whole number of 128-byte steps: products that repay the padded copies take the
+        # general path (biops_gemm_padded), the others the register loads here
+        m = input.numel() // k
+        aligned = (input.data_ptr() | weight.data_ptr()) % 16 == 0 and (k * elt) % 16 == 0 and \
+            (weight.stride(0) * elt) % 16 == 0
+        if m * n * k >= _PAD_MIN_WORK and (not aligned or k * elt >= _PAD_MIN_K_BYTES):
+            return None
     bias_ptr = None
     if bias is not None:
         if not (bias.is_cuda and bias.dim() == 1 and bias.dtype == dtype and bias.shape[0] == n

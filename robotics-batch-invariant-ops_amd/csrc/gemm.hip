@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "gemm.h"
 #include "gemm_big.h"
@@ -882,6 +883,129 @@ extern "C" int biops_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void
   a.lda = sAm; a.ldb = ldb; a.ldc = sCm;
   a.nb1 = 1; a.nb2 = 1; a.gB = 1;
   return launch_bmm(dtype, a, bias ? kEpiBias : kEpiPlain, kmajor, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ K padding ----
+// dst [rows_out, cols_out] = src [rows, cols] zero-extended; one 16-byte output chunk per thread
+// and iteration.  Whole chunks of a 16-byte aligned source are read with one load, others
+// element by element (a row of odd length is not 16-byte aligned after the first).
+struct PadArgs {
+  const void* src;
+  void* dst;
+  int64_t rows, cols, ld, rows_out, cols_out;
+  int32_t vec;  // src and ld * element size 16-byte aligned
+};
+
+template <int E>
+__global__ __launch_bounds__(256) void pad_rows_kernel(PadArgs a) {
+  using W = typename std::conditional<E == 2, uint16_t, uint32_t>::type;
+  constexpr int V = 16 / E;
+  const int64_t cpr = a.cols_out / V;
+  const int64_t total = a.rows_out * cpr;
+  const W* src = reinterpret_cast<const W*>(a.src);
+  W* dst = reinterpret_cast<W*>(a.dst);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cpr, k0 = (i - r * cpr) * V;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (r < a.rows && k0 < a.cols) {
+      const W* s = src + r * a.ld + k0;
+      if (a.vec && k0 + V <= a.cols) {
+        v = *reinterpret_cast<const u32x4_t*>(s);
+      } else {
+        W e[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) e[j] = k0 + j < a.cols ? s[j] : W(0);
+        v = __builtin_bit_cast(u32x4_t, e);
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(dst + r * a.cols_out + k0) = v;
+  }
+}
+
+static int pad_rows(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src, int64_t rows_out,
+                    int64_t cols_out, void* dst, hipStream_t stream) {
+  const int elt = dtype_bytes(dtype);
+  if (!is_float_dtype(dtype)) return fail(BIOPS_ERR_DTYPE, "unsupported dtype %d", dtype);
+  if (rows < 0 || cols < 0 || rows_out < rows || cols_out < cols)
+    return fail(BIOPS_ERR_ARG, "padded shape [%lld, %lld] smaller than [%lld, %lld]", (long long)rows_out,
+                (long long)cols_out, (long long)rows, (long long)cols);
+  if ((cols_out * elt) % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+    return fail(BIOPS_ERR_LAYOUT, "padded rows must be whole 16-byte chunks on a 16-byte aligned base");
+  if (rows > 1 && ld_src < cols) return fail(BIOPS_ERR_LAYOUT, "source rows overlap");
+  if (rows_out == 0 || cols_out == 0) return BIOPS_OK;
+  if (!dst || (rows > 0 && cols > 0 && !src)) return fail(BIOPS_ERR_ARG, "null operand");
+  PadArgs a{src, dst, rows, cols, ld_src, rows_out, cols_out, 0};
+  a.vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && (ld_src * elt) % 16 == 0;
+  const int64_t chunks = rows_out * (cols_out * elt / 16);
+  const int64_t blocks = std::min<int64_t>(cdiv(chunks, 256), 8192);
+  if (elt == 2)
+    hipLaunchKernelGGL(pad_rows_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(pad_rows_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  return check_launch("pad_rows_kernel");
+}
+
+extern "C" int biops_pad_rows(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src,
+                              int64_t rows_out, int64_t cols_out, void* dst, void* stream) {
+  return pad_rows(dtype, rows, cols, src, ld_src, rows_out, cols_out, dst, (hipStream_t)stream);
+}
+
+// Padded operands of biops_gemm_padded: A [M, Kp] at the workspace base, B [N, Kp] (K-major) or
+// [Kp, Np] (row-major, Np the row length rounded up to whole 16-byte chunks) 256 bytes further
+// on; Kp = K rounded up to a whole number of 128-byte steps.
+struct PadLayout {
+  int64_t kp, np, a_bytes, bytes;
+};
+static PadLayout pad_layout(int elt, int64_t M, int64_t N, int64_t K, bool kmajor) {
+  PadLayout p;
+  const int64_t step = kKBytes / elt;
+  p.kp = cdiv(K, step) * step;
+  p.np = kmajor ? N : cdiv(N * elt, 16) * 16 / elt;
+  p.a_bytes = cdiv(M * p.kp * elt, 256) * 256;
+  p.bytes = p.a_bytes + (kmajor ? N * p.kp : p.kp * p.np) * elt;
+  return p;
+}
+
+extern "C" int64_t biops_gemm_padded_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t sBk,
+                                                     int64_t sBn) {
+  bool kmajor;
+  int64_t ldb;
+  const int elt = dtype_bytes(dtype);
+  if (!is_float_dtype(dtype) || M < 0 || N < 0 || K < 0 || !b_layout(K, N, sBk, sBn, kmajor, ldb)) return -1;
+  return pad_layout(elt, M, N, K, kmajor).bytes;
+}
+
+extern "C" int biops_gemm_padded(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t sAm,
+                                 int64_t sAk, const void* B, int64_t sBk, int64_t sBn, const void* bias,
+                                 void* C, int64_t sCm, int64_t sCn, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  if (!is_float_dtype(dtype)) return fail(BIOPS_ERR_DTYPE, "unsupported dtype %d", dtype);
+  if (M < 0 || N < 0 || K < 0) return fail(BIOPS_ERR_ARG, "negative size");
+  if (M == 0 || N == 0) return BIOPS_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(BIOPS_ERR_ARG, "null operand");
+  if (sAk != 1 && K > 1) return fail(BIOPS_ERR_LAYOUT, "A must be contiguous in K");
+  if (sCn != 1 && N > 1) return fail(BIOPS_ERR_LAYOUT, "C must be contiguous in N");
+  bool kmajor;
+  int64_t ldb;
+  if (!b_layout(K, N, sBk, sBn, kmajor, ldb)) return fail(BIOPS_ERR_LAYOUT, "B needs a unit stride in K or in N");
+  const int elt = dtype_bytes(dtype);
+  const PadLayout p = pad_layout(elt, M, N, K, kmajor);
+  if (workspace_bytes < p.bytes)
+    return fail(BIOPS_ERR_SIZE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)p.bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(BIOPS_ERR_LAYOUT, "workspace must be 256-byte aligned");
+  char* ap = static_cast<char*>(workspace);
+  char* bp = ap + p.a_bytes;
+  const hipStream_t s = (hipStream_t)stream;
+  int rc = pad_rows(dtype, M, K, A, sAm, M, p.kp, ap, s);
+  if (rc != BIOPS_OK) return rc;
+  rc = kmajor ? pad_rows(dtype, N, K, B, ldb, N, p.kp, bp, s) : pad_rows(dtype, K, N, B, ldb, p.kp, p.np, bp, s);
+  if (rc != BIOPS_OK) return rc;
+  BmmArgs a{};
+  a.A = ap; a.B = bp; a.B2 = nullptr; a.C = C; a.bias = bias;
+  a.M = M; a.N = N; a.K = p.kp;
+  a.lda = p.kp; a.ldb = kmajor ? p.kp : p.np; a.ldc = sCm;
+  a.nb1 = 1; a.nb2 = 1; a.gB = 1;
+  return launch_bmm(dtype, a, bias ? kEpiBias : kEpiPlain, kmajor, s);
 }
 
 extern "C" int biops_gemm_tile_count(void) { return kMenuSize; }

@@ -1,4 +1,4 @@
-/* Fast-call CPython binding of the library's most frequent entry points (GEMM, row
+/* Fast-call CPython binding of the library's most frequent entry points (GEMM, padded GEMM, row
  * reductions, softmax, fused attention, the varlen planner and fused varlen attention), of
  * the host-to-device copy of the varlen work list and of the device-to-host copy of the MoE
  * index flag: the same C ABI as the ctypes binding,
@@ -75,6 +75,18 @@ static PyObject* fast_gemm(PyObject* self, PyObject* const* args, Py_ssize_t nar
   int rc;
   WITHOUT_GIL(rc, biops_gemm((int)iv[0], iv[1], iv[2], iv[3], pv[4], iv[5], iv[6], pv[7], iv[8], iv[9],
                                     pv[10], pv[11], iv[12], iv[13], pv[14]));
+  return PyLong_FromLong(rc);
+}
+
+/* gemm_padded(dtype, M, N, K, A, sAm, sAk, B, sBk, sBn, bias, C, sCm, sCn, workspace, bytes, stream) */
+static PyObject* fast_gemm_padded(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  int64_t iv[17];
+  void* pv[17];
+  (void)self;
+  if (!parse(args, nargs, "llllpllpllppllplp", iv, pv, NULL)) return NULL;
+  int rc;
+  WITHOUT_GIL(rc, biops_gemm_padded((int)iv[0], iv[1], iv[2], iv[3], pv[4], iv[5], iv[6], pv[7], iv[8], iv[9],
+                                    pv[10], pv[11], iv[12], iv[13], pv[14], iv[15], pv[16]));
   return PyLong_FromLong(rc);
 }
 
@@ -207,6 +219,7 @@ static PyObject* fast_copy_d2h(PyObject* self, PyObject* const* args, Py_ssize_t
 
 static PyMethodDef kMethods[] = {
     {"gemm", (PyCFunction)(void (*)(void))fast_gemm, METH_FASTCALL, "biops_gemm"},
+    {"gemm_padded", (PyCFunction)(void (*)(void))fast_gemm_padded, METH_FASTCALL, "biops_gemm_padded"},
     {"reduce", (PyCFunction)(void (*)(void))fast_reduce, METH_FASTCALL, "biops_reduce"},
     {"softmax", (PyCFunction)(void (*)(void))fast_softmax, METH_FASTCALL, "biops_softmax"},
     {"sdpa_fused", (PyCFunction)(void (*)(void))fast_sdpa_fused, METH_FASTCALL, "biops_sdpa_fused"},

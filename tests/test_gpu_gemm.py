@@ -384,3 +384,61 @@ def test_nmajor_b_matches_kmajor_bits(tile_menu, dtype, m, k, n):
     for cfg in range(tile_menu.biops_gemm_tile_count()):
         assert tile_menu.biops_set_gemm_tile(cfg) == 0
         assert_bitwise(matmul_persistent(x, b_rows), ref, f"tile entry {cfg}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("rows", "cols", "ld", "offset", "rows_out", "cols_out"), (
+    (5, 100, 100, 0, 5, 128),     # K tail only
+    (7, 1001, 1003, 1, 9, 1024),  # odd pitch, misaligned base, extra zero rows
+    (64, 64, 64, 0, 64, 64),      # nothing to pad: a plain copy
+    (3, 1, 5, 2, 4, 32),          # one column
+))
+def test_pad_rows_is_a_zero_extended_copy(dtype, rows, cols, ld, offset, rows_out, cols_out):
+    """biops_pad_rows copies [rows, cols] (row pitch ld) into [rows_out, cols_out] and writes
+    zeros everywhere else, whatever the alignment of the source."""
+    from batch_invariant_ops import _native as nat
+
+    flat = randn(offset + rows * ld + 8, seed=5600 + cols, dtype=dtype)
+    src = flat[offset:offset + rows * ld].view(rows, ld)[:, :cols]
+    expect = torch.zeros(rows_out, cols_out, dtype=dtype)
+    expect[:rows, :cols] = src
+    dflat = gpu(flat)
+    dst = torch.full((rows_out, cols_out), float("nan"), dtype=dtype, device="cuda")
+    nat.call("biops_pad_rows", nat.dtype_code(dtype), rows, cols, dflat.data_ptr() + offset * flat.element_size(),
+             ld, rows_out, cols_out, dst.data_ptr(), nat.stream_of(dst))
+    assert_bitwise(dst.cpu(), expect, "padded copy")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("m", "k", "n", "layout"), (
+    (300, 1000, 700, "w"),    # K % 64 != 0, rows 16-byte aligned
+    (257, 2050, 515, "w"),    # K % 8 != 0: unaligned rows
+    (64, 3000, 384, "rows"),  # row-major B: zero rows appended to B
+    (96, 1027, 130, "rows"),  # row-major B with N % 8 != 0: padded row pitch
+))
+def test_padded_k_gives_the_register_path_bits(monkeypatch, dtype, m, k, n, layout):
+    """Products whose K is not a whole number of 128-byte steps (or whose rows are not 16-byte
+    aligned) run on zero-padded copies (biops_gemm_padded) when large enough and on the
+    register load path otherwise; both give the same bits, so a row keeps its bits when the
+    batch crosses the size at which the copies start (batch invariance), and the result stays
+    within the GEMM bound of the oracle."""
+    import batch_invariant_ops.batch_invariant_ops as bio
+
+    x = gpu(randn(m, k, seed=5700 + k, dtype=dtype))
+    w = gpu(randn(n, k, seed=5701 + n, dtype=dtype) * 0.05)
+    b = w.t() if layout == "w" else w.t().contiguous()
+    bias = gpu(randn(n, seed=5702, dtype=dtype))
+    monkeypatch.setattr(bio, "_PAD_MIN_WORK", 1 << 62)
+    reg = matmul_persistent(x, b, bias)
+    one = matmul_persistent(x[m // 2:m // 2 + 1], b, bias)
+    monkeypatch.setattr(bio, "_PAD_MIN_WORK", 0)
+    monkeypatch.setattr(bio, "_PAD_MIN_K_BYTES", 0)
+    assert bio._padded_workspace(x, b, m, n, k) > 0
+    padded = matmul_persistent(x, b, bias)
+    assert_bitwise(padded, reg, "padded vs register path")
+    assert_bitwise(one, padded[m // 2:m // 2 + 1], "one row (register path) vs batch (padded)")
+    if layout == "w":
+        assert_bitwise(linear_batch_invariant(x, w, bias), reg, "linear shim")
+    ref = oracle.linear(x.cpu(), w.cpu(), bias.cpu()).double()
+    absprod = x.cpu().double().abs() @ w.cpu().double().abs().t() + bias.cpu().double().abs()
+    assert_gemm_close(padded.cpu(), ref, absprod, k)
