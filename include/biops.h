@@ -123,6 +123,19 @@ int biops_gemm_padded(int dtype, int64_t M, int64_t N, int64_t K,
                       void* workspace, int64_t workspace_bytes,
                       void* stream);
 
+/* biops_bmm_padded_workspace_size / biops_bmm_padded: the same for a batch of independent
+ * products C[b] = A[b] . B[b] (b < batch; batch strides sA, sB, sC in elements, 0 for an
+ * operand shared by every batch element, which is then copied once).  Same bits as biops_bmm
+ * with nb2 = gB = 1.  No counterpart in the reference. */
+int64_t biops_bmm_padded_workspace_size(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                                        int64_t sA, int64_t sB, int64_t sBk, int64_t sBn);
+int biops_bmm_padded(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                     const void* A, int64_t sA, int64_t sAm, int64_t sAk,
+                     const void* B, int64_t sB, int64_t sBk, int64_t sBn,
+                     void* C, int64_t sC, int64_t sCm, int64_t sCn,
+                     void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
 /* Number of entries in the GEMM tile menu.  Each entry is a (block tile, wavefront layout, LDS
  * ring depth) scheduling choice; all entries compute every output element with the same MFMA
  * sequence, so they produce identical bits and differ in speed only.  No reference

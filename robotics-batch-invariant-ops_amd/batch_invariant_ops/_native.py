@@ -49,6 +49,8 @@ _SIGNATURES = {
     "biops_pad_rows": (_i, [_i, _l, _l, _p, _l, _l, _l, _p, _p]),
     "biops_gemm_padded_workspace_size": (_l, [_i, _l, _l, _l, _l, _l]),
     "biops_gemm_padded": (_i, [_i, _l, _l, _l, _p, _l, _l, _p, _l, _l, _p, _p, _l, _l, _p, _l, _p]),
+    "biops_bmm_padded_workspace_size": (_l, [_i, _l, _l, _l, _l, _l, _l, _l, _l]),
+    "biops_bmm_padded": (_i, [_i, _l, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _p]),
     "biops_gemm_tile_count": (_i, []),
     "biops_set_gemm_tile": (_i, [_i]),
     "biops_softmax": (_i, [_i, _i, _l, _l, _p, _l, _p, _l, _i, _p]),

@@ -91,39 +91,48 @@ def _b_operand(b: torch.Tensor) -> torch.Tensor:
 
 
 # Products whose operands cannot take the direct global->LDS loads (K not a whole number of
-# 128-byte steps, or rows not 16-byte aligned) run through biops_gemm_padded, on zero-padded
-# copies, when they have at least this many multiply-adds and either misaligned rows (element
-# by element register loads) or rows of at least _PAD_MIN_K_BYTES; the others keep the register
-# load path of biops_gemm.  Both give the same bits: out-of-range K is zero in both operands on
-# every load path.  MI355X, bf16, per linear call (register path -> padded): 2048 x 2048 x 2050
-# 357 -> 42 us, 512 x 512 x 500 50 -> 26 us, 300 x 700 x 5000 77 -> 28 us, 1 x 4096 x 4000
-# 57 -> 27 us; with K = 1000 the register path was as fast or faster (256 x 1024 x 1000
-# 18 against 26 us).
+# 128-byte steps, or rows not 16-byte aligned) run through biops_gemm_padded / biops_bmm_padded,
+# on zero-padded copies, when they have at least _PAD_MIN_WORK multiply-adds and rows of at
+# least _PAD_MIN_K_BYTES (_PAD_MIN_MISALIGNED_K_BYTES when misaligned rows leave the register
+# path element-by-element loads); the others keep the register load path of biops_gemm /
+# biops_bmm.  Both give the same bits: out-of-range K is zero in both operands on every load
+# path.  MI355X, bf16, per call (register path -> padded): 2048 x 2048 x 2050 357 -> 42 us,
+# 512 x 512 x 500 50 -> 21 us, 300 x 700 x 5000 77 -> 28 us, 1 x 4096 x 4000 57 -> 27 us,
+# bmm 16 x 1024 x 2050 x 256 229 -> 73 us; the register path was as fast or faster with
+# aligned rows at K = 1000 (256 x 1024 x 1000 18 against 21 us) and with misaligned rows at
+# K = 100 (bmm 64 x 256 x 100 x 256 16.6 against 19.2 us).
 _PAD_MIN_WORK = 1 << 23
 _PAD_MIN_K_BYTES = 4000
+_PAD_MIN_MISALIGNED_K_BYTES = 512
 
 
 def _aligned16(t: torch.Tensor, ld: int) -> bool:
     return t.data_ptr() % 16 == 0 and (ld * t.element_size()) % 16 == 0
 
 
-def _padded_workspace(a: torch.Tensor, b: torch.Tensor, M: int, N: int, K: int) -> int:
+def _padded_workspace(a: torch.Tensor, b: torch.Tensor, M: int, N: int, K: int, batch: int = 0) -> int:
     """Workspace bytes of biops_gemm_padded for A [M, K] and B [K, N] (unit stride in K or N),
-    or 0 when the product should call biops_gemm on the operands as they are."""
+    or of biops_bmm_padded (``batch`` > 0) for A [batch, M, K] and B [batch, K, N]; 0 when the
+    product should run on the operands as they are."""
     elt = a.element_size()
     step = 128 // elt
-    kmajor = b.stride(0) == 1 or K <= 1
-    if not kmajor and b.stride(1) != 1 and N > 1:
+    kmajor = b.stride(-2) == 1 or K <= 1
+    if not kmajor and b.stride(-1) != 1 and N > 1:
         return 0
-    ldb = b.stride(1) if kmajor else b.stride(0)
-    aligned = _aligned16(a, a.stride(0)) and _aligned16(b, ldb) and (kmajor or (N * elt) % 16 == 0)
+    ldb = b.stride(-1) if kmajor else b.stride(-2)
+    aligned = (_aligned16(a, a.stride(-2)) and _aligned16(b, ldb) and (kmajor or (N * elt) % 16 == 0)
+               and (not batch or (a.stride(0) * elt) % 16 == 0 and (b.stride(0) * elt) % 16 == 0))
     if aligned and K % step == 0:
         return 0
-    if M * N * K < _PAD_MIN_WORK or (aligned and K * elt < _PAD_MIN_K_BYTES):
+    if max(batch, 1) * M * N * K < _PAD_MIN_WORK:
+        return 0
+    if K * elt < (_PAD_MIN_K_BYTES if aligned else _PAD_MIN_MISALIGNED_K_BYTES):
         return 0
     kp = -(-K // step) * step
     np_ = N if kmajor else -(-N * elt // 16) * 16 // elt
-    return -(-M * kp * elt // 256) * 256 + (N * kp if kmajor else kp * np_) * elt
+    na = 1 if not batch or a.stride(0) == 0 else batch
+    nb = 1 if not batch or b.stride(0) == 0 else batch
+    return -(-na * M * kp * elt // 256) * 256 + nb * (N * kp if kmajor else kp * np_) * elt
 
 
 def matmul_persistent(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = None):
@@ -194,13 +203,27 @@ def bmm_persistent(a: torch.Tensor, b: torch.Tensor):
         return c
     a = _k_contiguous(a, 2)
     b = _b_operand(b)
+    stream = nat.stream_of(c)
+    ws_bytes = _padded_workspace(a, b, m, n, k, batch) if k > 0 else 0
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, device=a.device, dtype=torch.uint8)
+        if ws.data_ptr() % 256 == 0:
+            nat.call(
+                "biops_bmm_padded",
+                nat.dtype_code(a.dtype), batch, m, n, k,
+                a.data_ptr(), a.stride(0), a.stride(1), a.stride(2),
+                b.data_ptr(), b.stride(0), b.stride(1), b.stride(2),
+                c.data_ptr(), c.stride(0), c.stride(1), c.stride(2),
+                ws.data_ptr(), ws_bytes, stream,
+            )
+            return c
     nat.call(
         "biops_bmm",
         nat.dtype_code(a.dtype), batch, 1, m, n, k,
         a.data_ptr(), a.stride(0), 0, a.stride(1), a.stride(2),
         b.data_ptr(), b.stride(0), 0, 1, b.stride(1), b.stride(2),
         c.data_ptr(), c.stride(0), 0, c.stride(1), c.stride(2),
-        nat.stream_of(c),
+        stream,
     )
     return c
 
@@ -248,7 +271,7 @@ def _linear_direct(input, weight, bias):
         m = input.numel() // k
         aligned = (input.data_ptr() | weight.data_ptr()) % 16 == 0 and (k * elt) % 16 == 0 and \
             (weight.stride(0) * elt) % 16 == 0
-        if m * n * k >= _PAD_MIN_WORK and (not aligned or k * elt >= _PAD_MIN_K_BYTES):
+        if m * n * k >= _PAD_MIN_WORK and k * elt >= (_PAD_MIN_K_BYTES if aligned else _PAD_MIN_MISALIGNED_K_BYTES):
             return None
     bias_ptr = None
     if bias is not None:

@@ -893,7 +893,8 @@ struct PadArgs {
   const void* src;
   void* dst;
   int64_t rows, cols, ld, rows_out, cols_out;
-  int32_t vec;  // src and ld * element size 16-byte aligned
+  int64_t batches, sbatch;  // source matrices and their stride (elements); destinations follow each other
+  int32_t vec;              // src, ld and sbatch 16-byte aligned
 };
 
 template <int E>
@@ -901,14 +902,16 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(PadArgs a) {
   using W = typename std::conditional<E == 2, uint16_t, uint32_t>::type;
   constexpr int V = 16 / E;
   const int64_t cpr = a.cols_out / V;
-  const int64_t total = a.rows_out * cpr;
+  const int64_t per = a.rows_out * cpr;  // chunks of one destination matrix
+  const int64_t total = a.batches * per;
   const W* src = reinterpret_cast<const W*>(a.src);
   W* dst = reinterpret_cast<W*>(a.dst);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / cpr, k0 = (i - r * cpr) * V;
+    const int64_t b = i / per, j = i - b * per;
+    const int64_t r = j / cpr, k0 = (j - r * cpr) * V;
     u32x4_t v = {0u, 0u, 0u, 0u};
     if (r < a.rows && k0 < a.cols) {
-      const W* s = src + r * a.ld + k0;
+      const W* s = src + b * a.sbatch + r * a.ld + k0;
       if (a.vec && k0 + V <= a.cols) {
         v = *reinterpret_cast<const u32x4_t*>(s);
       } else {
@@ -918,12 +921,12 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(PadArgs a) {
         v = __builtin_bit_cast(u32x4_t, e);
       }
     }
-    *reinterpret_cast<u32x4_t*>(dst + r * a.cols_out + k0) = v;
+    *reinterpret_cast<u32x4_t*>(dst + i * V) = v;
   }
 }
 
 static int pad_rows(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src, int64_t rows_out,
-                    int64_t cols_out, void* dst, hipStream_t stream) {
+                    int64_t cols_out, void* dst, hipStream_t stream, int64_t batches = 1, int64_t sbatch = 0) {
   const int elt = dtype_bytes(dtype);
   if (!is_float_dtype(dtype)) return fail(BIOPS_ERR_DTYPE, "unsupported dtype %d", dtype);
   if (rows < 0 || cols < 0 || rows_out < rows || cols_out < cols)
@@ -934,9 +937,9 @@ static int pad_rows(int dtype, int64_t rows, int64_t cols, const void* src, int6
   if (rows > 1 && ld_src < cols) return fail(BIOPS_ERR_LAYOUT, "source rows overlap");
   if (rows_out == 0 || cols_out == 0) return BIOPS_OK;
   if (!dst || (rows > 0 && cols > 0 && !src)) return fail(BIOPS_ERR_ARG, "null operand");
-  PadArgs a{src, dst, rows, cols, ld_src, rows_out, cols_out, 0};
-  a.vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && (ld_src * elt) % 16 == 0;
-  const int64_t chunks = rows_out * (cols_out * elt / 16);
+  PadArgs a{src, dst, rows, cols, ld_src, rows_out, cols_out, batches, sbatch, 0};
+  a.vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && (ld_src * elt) % 16 == 0 && (sbatch * elt) % 16 == 0;
+  const int64_t chunks = batches * rows_out * (cols_out * elt / 16);
   const int64_t blocks = std::min<int64_t>(cdiv(chunks, 256), 8192);
   if (elt == 2)
     hipLaunchKernelGGL(pad_rows_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
@@ -1006,6 +1009,61 @@ extern "C" int biops_gemm_padded(int dtype, int64_t M, int64_t N, int64_t K, con
   a.lda = p.kp; a.ldb = kmajor ? p.kp : p.np; a.ldc = sCm;
   a.nb1 = 1; a.nb2 = 1; a.gB = 1;
   return launch_bmm(dtype, a, bias ? kEpiBias : kEpiPlain, kmajor, s);
+}
+
+// biops_bmm_padded: one padded copy per distinct batch matrix (a stride-0 operand is copied once).
+static PadLayout pad_layout_batched(int elt, int64_t na, int64_t nb, int64_t M, int64_t N, int64_t K, bool kmajor) {
+  PadLayout p = pad_layout(elt, M, N, K, kmajor);
+  p.a_bytes = cdiv(na * M * p.kp * elt, 256) * 256;
+  p.bytes = p.a_bytes + nb * (kmajor ? N * p.kp : p.kp * p.np) * elt;
+  return p;
+}
+
+extern "C" int64_t biops_bmm_padded_workspace_size(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                                                    int64_t sA, int64_t sB, int64_t sBk, int64_t sBn) {
+  bool kmajor;
+  int64_t ldb;
+  const int elt = dtype_bytes(dtype);
+  if (!is_float_dtype(dtype) || batch < 0 || M < 0 || N < 0 || K < 0 || !b_layout(K, N, sBk, sBn, kmajor, ldb))
+    return -1;
+  return pad_layout_batched(elt, sA == 0 ? 1 : batch, sB == 0 ? 1 : batch, M, N, K, kmajor).bytes;
+}
+
+extern "C" int biops_bmm_padded(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A, int64_t sA,
+                                int64_t sAm, int64_t sAk, const void* B, int64_t sB, int64_t sBk, int64_t sBn,
+                                void* C, int64_t sC, int64_t sCm, int64_t sCn, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  if (!is_float_dtype(dtype)) return fail(BIOPS_ERR_DTYPE, "unsupported dtype %d", dtype);
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(BIOPS_ERR_ARG, "negative size");
+  if (batch == 0 || M == 0 || N == 0) return BIOPS_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(BIOPS_ERR_ARG, "null operand");
+  if (sAk != 1 && K > 1) return fail(BIOPS_ERR_LAYOUT, "A must be contiguous in K");
+  if (sCn != 1 && N > 1) return fail(BIOPS_ERR_LAYOUT, "C must be contiguous in N");
+  bool kmajor;
+  int64_t ldb;
+  if (!b_layout(K, N, sBk, sBn, kmajor, ldb)) return fail(BIOPS_ERR_LAYOUT, "B needs a unit stride in K or in N");
+  const int elt = dtype_bytes(dtype);
+  const int64_t na = sA == 0 ? 1 : batch, nb = sB == 0 ? 1 : batch;
+  const PadLayout p = pad_layout_batched(elt, na, nb, M, N, K, kmajor);
+  if (workspace_bytes < p.bytes)
+    return fail(BIOPS_ERR_SIZE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)p.bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(BIOPS_ERR_LAYOUT, "workspace must be 256-byte aligned");
+  char* ap = static_cast<char*>(workspace);
+  char* bp = ap + p.a_bytes;
+  const hipStream_t s = (hipStream_t)stream;
+  int rc = pad_rows(dtype, M, K, A, sAm, M, p.kp, ap, s, na, sA);
+  if (rc != BIOPS_OK) return rc;
+  rc = kmajor ? pad_rows(dtype, N, K, B, ldb, N, p.kp, bp, s, nb, sB) : pad_rows(dtype, K, N, B, ldb, p.kp, p.np, bp, s, nb, sB);
+  if (rc != BIOPS_OK) return rc;
+  BmmArgs a{};
+  a.A = ap; a.B = bp; a.B2 = nullptr; a.C = C; a.bias = nullptr;
+  a.M = M; a.N = N; a.K = p.kp;
+  a.lda = p.kp; a.ldb = kmajor ? p.kp : p.np; a.ldc = sCm;
+  a.nb1 = batch; a.nb2 = 1; a.gB = 1;
+  a.sA1 = na == 1 ? 0 : M * p.kp;
+  a.sB1 = nb == 1 ? 0 : (kmajor ? N * p.kp : p.kp * p.np);
+  a.sC1 = sC;
+  return launch_bmm(dtype, a, kEpiPlain, kmajor, s);
 }
 
 extern "C" int biops_gemm_tile_count(void) { return kMenuSize; }

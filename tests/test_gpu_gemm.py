@@ -433,6 +433,7 @@ def test_padded_k_gives_the_register_path_bits(monkeypatch, dtype, m, k, n, layo
     one = matmul_persistent(x[m // 2:m // 2 + 1], b, bias)
     monkeypatch.setattr(bio, "_PAD_MIN_WORK", 0)
     monkeypatch.setattr(bio, "_PAD_MIN_K_BYTES", 0)
+    monkeypatch.setattr(bio, "_PAD_MIN_MISALIGNED_K_BYTES", 0)
     assert bio._padded_workspace(x, b, m, n, k) > 0
     padded = matmul_persistent(x, b, bias)
     assert_bitwise(padded, reg, "padded vs register path")
@@ -442,3 +443,35 @@ def test_padded_k_gives_the_register_path_bits(monkeypatch, dtype, m, k, n, layo
     ref = oracle.linear(x.cpu(), w.cpu(), bias.cpu()).double()
     absprod = x.cpu().double().abs() @ w.cpu().double().abs().t() + bias.cpu().double().abs()
     assert_gemm_close(padded.cpu(), ref, absprod, k)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("batch", "m", "k", "n", "layout"), (
+    (4, 100, 2050, 130, "cols"),   # unaligned rows, K-major B
+    (3, 64, 1000, 256, "rows"),    # K % 64 != 0, row-major B
+    (5, 40, 333, 72, "shared"),    # A shared by every batch element (stride 0): copied once
+))
+def test_bmm_padded_k_gives_the_register_path_bits(monkeypatch, dtype, batch, m, k, n, layout):
+    """bmm_persistent through biops_bmm_padded (zero-padded copies of the batch's operands)
+    gives the bits of the register load path, for one batch element alone as well, and stays
+    within the GEMM bound of the oracle."""
+    import batch_invariant_ops.batch_invariant_ops as bio
+
+    if layout == "shared":
+        a_cpu = randn(1, m, k, seed=5800 + k, dtype=dtype).expand(batch, m, k)
+    else:
+        a_cpu = randn(batch, m, k, seed=5800 + k, dtype=dtype)
+    b_cpu = randn(batch, k, n, seed=5801 + n, dtype=dtype) * 0.05
+    a = gpu(a_cpu.contiguous())[:1].expand(batch, m, k) if layout == "shared" else gpu(a_cpu)
+    b = gpu(b_cpu).transpose(1, 2).contiguous().transpose(1, 2) if layout == "cols" else gpu(b_cpu)
+    monkeypatch.setattr(bio, "_PAD_MIN_WORK", 1 << 62)
+    reg = bmm_persistent(a, b)
+    monkeypatch.setattr(bio, "_PAD_MIN_WORK", 0)
+    monkeypatch.setattr(bio, "_PAD_MIN_K_BYTES", 0)
+    monkeypatch.setattr(bio, "_PAD_MIN_MISALIGNED_K_BYTES", 0)
+    assert bio._padded_workspace(a, b, m, n, k, batch) > 0
+    padded = bmm_persistent(a, b)
+    assert_bitwise(padded, reg, "padded vs register path")
+    assert_bitwise(bmm_persistent(a[1:2], b[1:2]), reg[1:2], "one batch element")
+    ref = oracle.bmm(a_cpu.contiguous(), b_cpu)
+    assert_gemm_close(padded, ref, a_cpu.double().abs() @ b_cpu.double().abs(), k)
