@@ -219,8 +219,8 @@ void bmm_kernel(BmmArgs args) {
   }
 }
 
-// One 32 x BC block per workgroup; wavefront 0 stores it straight from the accumulators with
-// the rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
+// One 32 x BC block per workgroup; each computing wavefront stores its part straight from the
+// accumulators with the rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
 template <typename T, int AR, int BC>
 __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   using S = SkinnyTile<T, AR, BC>;
@@ -236,12 +236,14 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   const int rows = rows64 < 32 ? (int)rows64 : 32;
   const int cols = cols64 < BC ? (int)cols64 : BC;
   const typename S::Acc acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
-  const int w = threadIdx.x >> 6;  // computing wavefront w stores columns 32w .. 32w+31
+  const int w = threadIdx.x >> 6;
   if (w >= S::CW) return;
-  const int64_t n0 = o.n0 + 32 * w;
-  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + o.m0 * args.ldc + n0;
+  const int wr = w / S::CWC, wc = w % S::CWC;
+  const int64_t n0 = o.n0 + S::WC * wc;
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + (o.m0 + S::WR * wr) * args.ldc + n0;
   const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
-  S::Math::store(acc, Cp, args.ldc, rows, cols - 32 * w, bias);
+  const int wrows = rows - S::WR * wr, wcols = cols - S::WC * wc;
+  S::Math::store(acc, Cp, args.ldc, wrows < S::WR ? wrows : S::WR, wcols < S::WC ? wcols : S::WC, bias);
 }
 
 template <typename T, int BM, int BN, int SB, bool BKM>

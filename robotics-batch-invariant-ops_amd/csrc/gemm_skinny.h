@@ -1,9 +1,10 @@
 // Skinny GEMM tile for problems with few rows (decode-size linears): one 32 x BC block per
 // workgroup, used when all blocks of a launch fit one round on the compute units.
 //
-// One workgroup owns one 32 x BC output block (BC = 64, 32, 16 or 8 columns).  Wavefront 0
-// (wavefronts 0 and 1 for 64 columns, 32 each) computes it over K steps of 128 bytes in order,
-// with the arithmetic of SkinnyMath below (bits equal to those of every other tile entry).  What differs is how operands arrive: eight
+// One workgroup owns one 32 x BC output block (BC = 64, 32, 16 or 8 columns).  Up to eight of
+// its wavefronts compute it, each a 16- or 32-row by 8- to 32-column part, over K steps of 128
+// bytes in order, with the arithmetic of SkinnyMath below (bits equal to those of every other
+// tile entry).  What differs is how operands arrive: eight
 // wavefronts share the 1 KiB global->LDS load instructions of a stage (4 or 8 K steps, 512 or
 // 1024 bytes of every row) round-robin, into a ring of 2-4 stages (up to the 160 KiB of a
 // compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate
@@ -158,9 +159,19 @@ struct SkinnyTile {
   static_assert(AR == 8 || AR == 16 || AR == 32, "A rows per K step");
   static_assert(BC == 8 || BC == 16 || BC == 32 || BC == 64, "B columns per K step");
   static constexpr int WAVES = 8;
-  // Wavefronts that compute: one per 32 columns of the block (a 64-column block splits its
-  // MFMA chains over two); all eight load.
-  static constexpr int CW = BC > 32 ? BC / 32 : 1;
+  // The block's MFMA chains are split over CW computing wavefronts of WR rows x WC columns
+  // (whole 16-row / 16-column sub-blocks, so that the lds_off swizzle of a wavefront's rows and
+  // columns is that of rows / columns 0..15); all eight wavefronts load.  16-bit types: 16
+  // columns per wavefront from 32-column blocks on, and 16 rows for 32-row blocks of at most 32
+  // columns; fp32 keeps whole 32x32 blocks (32 columns each for 64-column blocks).  Measured on
+  // MI355X (bf16, same-box A/B, same bits; one computing wavefront per 32 columns before):
+  // 128 x 2048 x 8192 (32 x 32 blocks, 4 wavefronts) 20.3 -> 14.8 us, 32 x 2048 x 8192 (32 x 8,
+  // 2) 12.9 -> 11.5 us, 64 x 2048 x 8192 (32 x 16, 2) 12.8 -> 11.6 us, 32 x 8192 x 2048 (32 x 32)
+  // 8.3 -> 6.8 us, 256 x 2048 x 8192 (32 x 64, 4) 27.2 -> 24.8 us (25.9 with 8 of 16 x 16).
+  static constexpr int WC = sizeof(T) == 2 ? (BC >= 32 ? 16 : BC) : (BC > 32 ? 32 : BC);
+  static constexpr int WR = sizeof(T) == 2 ? (AR >= 32 && BC <= 32 ? 16 : AR) : AR;
+  static constexpr int CWC = BC / WC;
+  static constexpr int CW = (AR / WR) * CWC;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int BK = kKBytes / (int)sizeof(T);
@@ -201,14 +212,15 @@ struct SkinnyTile {
     asm volatile("" ::: "memory");
   }
 
-  using Math = SkinnyMath<T, AR, BC>;
+  using Math = SkinnyMath<T, WR, WC>;
   using Acc = typename Math::Acc;
   using Frags = typename Math::Frags;
-  // Computing wavefront w reads columns 32w .. 32w+31 (the lds_off swizzle of a column only
-  // depends on its index modulo 16).
+  // Computing wavefront w reads rows WR (w / CWC) .. + WR-1 and columns WC (w % CWC) .. + WC-1
+  // (the lds_off swizzle of a row or column only depends on its index modulo 16).
   __device__ static __forceinline__ void load_frags(const char* kstep, Frags& f) {
-    const int bofs = CW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 32 * kKBytes : 0;
-    Math::load(kstep, LDS_A + bofs, f);
+    const int w = CW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    const int aofs = (w / CWC) * WR * kKBytes, bofs = (w % CWC) * WC * kKBytes;
+    Math::load(kstep + aofs, LDS_A + bofs - aofs, f);
   }
   __device__ static __forceinline__ void mfma(Acc& acc, const Frags& f) {
 #pragma unroll
@@ -238,7 +250,7 @@ struct SkinnyTile {
   // The 32 x BC block at (A, B) with `rows` / `cols` valid rows and columns (>= 1) over KT K
   // steps.  Stage s holds K steps s*U .. s*U+U-1 (the last stage may hold fewer).  The U*IPK
   // 1 KiB load instructions of a stage (K step u, part p: A rows 8p..8p+7 or B columns) are
-  // dealt round-robin to the 8 wavefronts.  Returns the accumulator of columns 32w .. 32w+31
+  // dealt round-robin to the 8 wavefronts.  Returns the accumulator of its part of the block
   // in computing wavefront w < CW (the other wavefronts return zeros once their last load is
   // issued; the kernel only lets the computing wavefronts continue).
   __device__ static __forceinline__ Acc run(char* smem, const T* A, int64_t lda, int rows,
