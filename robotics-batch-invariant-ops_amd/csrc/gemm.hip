@@ -228,12 +228,13 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   __shared__ __attribute__((aligned(16))) char smem[S::LDS_BYTES];
   const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
   if (t >= (uint32_t)args.total) return;
-  const TileOrigin o = tile_origin(args, t, 32, BC);
+  constexpr int BH = AR > 32 ? 64 : 32;  // block rows
+  const TileOrigin o = tile_origin(args, t, BH, BC);
   const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
   const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
                (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
   const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
-  const int rows = rows64 < 32 ? (int)rows64 : 32;
+  const int rows = rows64 < BH ? (int)rows64 : BH;
   const int cols = cols64 < BC ? (int)cols64 : BC;
   const typename S::Acc acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
   const int w = threadIdx.x >> 6;
@@ -383,10 +384,15 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
   // automatic choice before them, same bits: 256 x 2048 x 8192 33.7 -> 26.8 us, 128 x 4096 x
   // 4096 18.3 -> 15.6 us, 512 x 1024 x 4096 18.3 -> 15.5 us, 96 x 5000 x 2048 11.6 -> 10.1 us,
   // 512 x 1024 x 1024 7.9 -> 7.3 us; with one row block or K = 512 they lost: 32 x 16384 x
-  // 2048 13.0 -> 14.0 us, 64 x 8192 x 512 6.0 -> 6.3 us).
-  const int64_t row_blocks = batch * cdiv(a.M, 32);
+  // 2048 13.0 -> 14.0 us, 64 x 8192 x 512 6.0 -> 6.3 us), or, for 16-bit types, 64-row blocks
+  // of 32 or 64 columns in one round with 2 to 8 of them down M (512 x 2048 x 8192 38.4 ->
+  // 33.0 us, 300 x 3000 x 2048 11.7 -> 10.3 us, 128 x 8192 x 2048 12.7 -> 12.2 us; 16 down M
+  // lost: 1024 x 1024 x 4096 19.0 -> 19.8 us).
+  const int64_t row_blocks = batch * cdiv(a.M, 32), row_blocks64 = batch * cdiv(a.M, 64);
   if (skinny_ok && (row_blocks * cdiv(a.N, 32) <= cus ||
-                    (row_blocks >= 2 && a.K >= 1024 && row_blocks * cdiv(a.N, 64) <= cus)))
+                    (row_blocks >= 2 && a.K >= 1024 && row_blocks * cdiv(a.N, 64) <= cus) ||
+                    (dtype != BIOPS_F32 && row_blocks64 >= 2 && row_blocks64 <= 8 && a.K >= 1024 &&
+                     row_blocks64 * cdiv(a.N, 64) <= cus)))
     best = kSkinnyCfg;
   // Grouped rows of at most 56 rows per group on average with a 16-bit N-major B (the MoE
   // expert GEMMs of calls up to about 7E/k tokens): the weight-streaming entries.  MI355X, C5
@@ -404,7 +410,7 @@ static int pick_cfg(int dtype, const BmmArgs& a, int epi, bool skinny_ok, bool n
 template <typename T, int AR, int BC>
 static int launch_skinny_block(const BmmArgs& a0, hipStream_t stream) {
   BmmArgs a = a0;
-  a.tiles_m = cdiv(a.M, 32);
+  a.tiles_m = cdiv(a.M, AR > 32 ? 64 : 32);
   a.tiles_n = cdiv(a.N, BC);
   a.total = a.nb1 * a.nb2 * a.tiles_m * a.tiles_n;
   if (a.total == 0) return BIOPS_OK;
@@ -501,6 +507,15 @@ template <typename T>
 static int launch_skinny(const BmmArgs& a, hipStream_t stream) {
   if (a.M <= 8) return launch_skinny_rows<T, 8>(a, stream);
   if (a.M <= 16) return launch_skinny_rows<T, 16>(a, stream);
+  // 64-row blocks (16-bit types) where 32-row blocks of up to 64 columns take more than one
+  // round and 64-row ones fit it (pick_cfg's rule)
+  if constexpr (sizeof(T) == 2) {
+    const int64_t cus = device_cus(), batch = a.nb1 * a.nb2;
+    if (batch * cdiv(a.M, 32) * cdiv(a.N, 64) > cus && batch * cdiv(a.M, 64) * cdiv(a.N, 64) <= cus) {
+      if (batch * cdiv(a.M, 64) * cdiv(a.N, 32) <= cus) return launch_skinny_block<T, 64, 32>(a, stream);
+      return launch_skinny_block<T, 64, 64>(a, stream);
+    }
+  }
   return launch_skinny_rows<T, 32>(a, stream);
 }
 

@@ -1,10 +1,12 @@
-// Skinny GEMM tile for problems with few rows (decode-size linears): one 32 x BC block per
-// workgroup, used when all blocks of a launch fit one round on the compute units.
+// Skinny GEMM tile for problems with few rows (decode-size linears): one 32 x BC (or, 16-bit
+// types, 64 x BC) block per workgroup, used when all blocks of a launch fit one round on the
+// compute units.
 //
-// One workgroup owns one 32 x BC output block (BC = 64, 32, 16 or 8 columns).  Up to eight of
-// its wavefronts compute it, each a 16- or 32-row by 8- to 32-column part, over K steps of 128
-// bytes in order, with the arithmetic of SkinnyMath below (bits equal to those of every other
-// tile entry).  What differs is how operands arrive: eight
+// One workgroup owns one 32 x BC output block (BC = 64, 32, 16 or 8 columns; 64 x 32 and
+// 64 x 64 blocks load AR = 64 rows).  Up to eight of its wavefronts compute it, each a 16- or
+// 32-row by 8- to 32-column part, over K steps of 128 bytes in order, with the arithmetic of
+// SkinnyMath below (bits equal to those of every other tile entry).  What differs is how
+// operands arrive: eight
 // wavefronts share the 1 KiB global->LDS load instructions of a stage (4 or 8 K steps, 512 or
 // 1024 bytes of every row) round-robin, into a ring of 2-4 stages (up to the 160 KiB of a
 // compute unit), and one barrier per stage publishes it.  On MI355X a compute unit's load rate
@@ -14,8 +16,9 @@
 // chain of its accumulator and the bytes it streams; the ring keeps the stream ahead of the
 // chain.
 //
-// Only AR A rows are loaded (AR = 8, 16 or 32, the rows a block can hold); MFMA rows past AR
-// read loaded rows again (row r reads row r mod AR) and, like rows past M, are never stored.
+// Only AR A rows are loaded (AR = 8, 16 or 32 for 32-row blocks, the rows a block can hold);
+// MFMA rows past AR read loaded rows again (row r reads row r mod AR) and, like rows past M,
+// are never stored.
 // Likewise only BC B columns are loaded and MFMA column c reads column c mod BC.  An MFMA output
 // element depends on its own A row and B column only, so the BC stored columns carry the bits
 // of a full 32-column block; narrow blocks spread a few-column-block problem (N = 2048: 64
@@ -156,7 +159,7 @@ struct SkinnyMath<T, AR, BC, false> {
 
 template <typename T, int AR, int BC>
 struct SkinnyTile {
-  static_assert(AR == 8 || AR == 16 || AR == 32, "A rows per K step");
+  static_assert(AR == 8 || AR == 16 || AR == 32 || AR == 64, "A rows per K step");
   static_assert(BC == 8 || BC == 16 || BC == 32 || BC == 64, "B columns per K step");
   static constexpr int WAVES = 8;
   // The block's MFMA chains are split over CW computing wavefronts of WR rows x WC columns
@@ -169,7 +172,7 @@ struct SkinnyTile {
   // 2) 12.9 -> 11.5 us, 64 x 2048 x 8192 (32 x 16, 2) 12.8 -> 11.6 us, 32 x 8192 x 2048 (32 x 32)
   // 8.3 -> 6.8 us, 256 x 2048 x 8192 (32 x 64, 4) 27.2 -> 24.8 us (25.9 with 8 of 16 x 16).
   static constexpr int WC = sizeof(T) == 2 ? (BC >= 32 ? 16 : BC) : (BC > 32 ? 32 : BC);
-  static constexpr int WR = sizeof(T) == 2 ? (AR >= 32 && BC <= 32 ? 16 : AR) : AR;
+  static constexpr int WR = AR > 32 ? 32 : (sizeof(T) == 2 && AR == 32 && BC <= 32 ? 16 : AR);
   static constexpr int CWC = BC / WC;
   static constexpr int CW = (AR / WR) * CWC;
   static constexpr int THREADS = 64 * WAVES;

@@ -338,15 +338,18 @@ def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 @pytest.mark.parametrize(("m", "n", "k"), (
     (256, 2048, 2048),   # 8 row blocks x 32 blocks of 64 columns: one round
-    (64, 8100, 1024),    # 2 x 127 blocks, 36-column last block (wavefront 1 stores 4 columns)
-    (256, 2000, 1024),   # 16-column last block: wavefront 1 of that block stores nothing
+    (64, 8100, 1024),    # 2 x 127 blocks, 36-column last block (its third 16-column part stores 4)
+    (256, 2000, 1024),   # 16-column last block: three of its four column parts store nothing
     (33, 16384, 1024),   # 2 x 256 blocks: more than one round, forced
+    (512, 2048, 1024),   # 16-bit types: 8 x 32 blocks of 64 rows x 64 columns
+    (128, 4096, 1024),   # 16-bit types: 2 x 128 blocks of 64 x 32
+    (300, 3000, 1024),   # 16-bit types: 5 x 47 blocks of 64 x 64, partial last rows and columns
 ))
 def test_skinny_64_column_blocks_give_identical_bits(tile_menu, dtype, m, n, k):
-    """With at least two row blocks the skinny entry also takes 64-column blocks, split over two
-    computing wavefronts of 32 columns each; rows keep the bits of entry 2, with and without a
-    bias, and of a call on the last row alone.  The automatic choice takes them where they fit
-    one round."""
+    """With at least two row blocks the skinny entry also takes 64-column blocks (and, for 16-bit
+    types, 64-row blocks), their MFMA chains split over several computing wavefronts; rows keep
+    the bits of entry 2, with and without a bias, and of a call on the last row alone.  The
+    automatic choice takes them where they fit one round."""
     x = gpu(randn(m, k, seed=5500 + m, dtype=dtype))
     w = gpu(randn(n, k, seed=5501 + n, dtype=dtype) * 0.05)
     bias = gpu(randn(n, seed=5502, dtype=dtype))
