@@ -226,6 +226,33 @@ def test_workspace_queries():
     assert L.biops_moe_workspace_size(9, 1, 1, 1, 1) == -1
 
 
+def test_padded_workspace_rule_matches_the_library():
+    """The Python wrappers size the workspace of biops_gemm_padded / biops_bmm_padded themselves
+    (no extra call per product); their sizes must equal the library's for every layout, and the
+    rule must leave direct-load operands alone and pad long or misaligned K of large products."""
+    L = lib()
+    codes = {torch.bfloat16: nat.BF16, torch.float16: nat.F16, torch.float32: nat.F32}
+    for dt, M, N, K in ((torch.bfloat16, 300, 700, 5000), (torch.float16, 257, 515, 2050),
+                        (torch.float32, 64, 8192, 2040), (torch.bfloat16, 96, 130, 1027)):
+        a = torch.zeros(M, K, dtype=dt)
+        for b in (torch.zeros(N, K, dtype=dt).t(), torch.zeros(K, N, dtype=dt)):
+            ws = bio_ops._padded_workspace(a, b, M, N, K)
+            assert ws > 0, (dt, M, N, K, b.stride())
+            assert ws == L.biops_gemm_padded_workspace_size(codes[dt], M, N, K, b.stride(0), b.stride(1))
+        a3 = torch.zeros(3, M, K, dtype=dt)
+        for b3 in (torch.zeros(3, N, K, dtype=dt).transpose(1, 2), torch.zeros(3, K, N, dtype=dt),
+                   torch.zeros(1, K, N, dtype=dt).expand(3, K, N)):
+            ws = bio_ops._padded_workspace(a3, b3, M, N, K, 3)
+            assert ws == L.biops_bmm_padded_workspace_size(codes[dt], 3, M, N, K, a3.stride(0), b3.stride(0),
+                                                           b3.stride(1), b3.stride(2))
+    # whole 128-byte steps on aligned rows, and small products, keep biops_gemm
+    assert bio_ops._padded_workspace(torch.zeros(64, 2048, dtype=torch.bfloat16),
+                                 torch.zeros(2048, 512, dtype=torch.bfloat16), 64, 512, 2048) == 0
+    assert bio_ops._padded_workspace(torch.zeros(32, 80, dtype=torch.bfloat16),
+                                 torch.zeros(80, 512, dtype=torch.bfloat16), 32, 512, 80) == 0
+    assert L.biops_gemm_padded_workspace_size(9, 1, 1, 1, 1, 1) == -1
+
+
 def plan(cu_q, cu_kv, hq=4, dv=24, dtype=nat.BF16):
     L = lib()
     n = len(cu_q) - 1
