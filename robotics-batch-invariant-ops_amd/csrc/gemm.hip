@@ -219,8 +219,22 @@ void bmm_kernel(BmmArgs args) {
   }
 }
 
-// One 32 x BC block per workgroup; each computing wavefront stores its part straight from the
-// accumulators with the rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
+// Computing wavefront w < CW of a skinny block stores its part straight from the accumulators
+// with the rounding of the LDS-staged epilogue: round(acc (+ bias[n])).
+template <typename S, typename T>
+__device__ __forceinline__ void skinny_store(const BmmArgs& args, const TileOrigin& o, int rows, int cols,
+                                             const typename S::Acc& acc) {
+  const int w = threadIdx.x >> 6;
+  if (w >= S::CW) return;
+  const int wr = w / S::CWC, wc = w % S::CWC;
+  const int64_t n0 = o.n0 + S::WC * wc;
+  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + (o.m0 + S::WR * wr) * args.ldc + n0;
+  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
+  const int wrows = rows - S::WR * wr, wcols = cols - S::WC * wc;
+  S::Math::store(acc, Cp, args.ldc, wrows < S::WR ? wrows : S::WR, wcols < S::WC ? wcols : S::WC, bias);
+}
+
+// One 32 x BC (or 64 x BC) block per workgroup.
 template <typename T, int AR, int BC>
 __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   using S = SkinnyTile<T, AR, BC>;
@@ -237,14 +251,27 @@ __global__ __launch_bounds__(512) void skinny_kernel(BmmArgs args) {
   const int rows = rows64 < BH ? (int)rows64 : BH;
   const int cols = cols64 < BC ? (int)cols64 : BC;
   const typename S::Acc acc = S::run(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
-  const int w = threadIdx.x >> 6;
-  if (w >= S::CW) return;
-  const int wr = w / S::CWC, wc = w % S::CWC;
-  const int64_t n0 = o.n0 + S::WC * wc;
-  T* Cp = reinterpret_cast<T*>(args.C) + o.b1 * args.sC1 + o.b2 * args.sC2 + (o.m0 + S::WR * wr) * args.ldc + n0;
-  const T* bias = args.bias ? reinterpret_cast<const T*>(args.bias) + n0 : nullptr;
-  const int wrows = rows - S::WR * wr, wcols = cols - S::WC * wc;
-  S::Math::store(acc, Cp, args.ldc, wrows < S::WR ? wrows : S::WR, wcols < S::WC ? wcols : S::WC, bias);
+  skinny_store<S, T>(args, o, rows, cols, acc);
+}
+
+// The same blocks on the loader-split schedule (SkinnyTile::run_deep): CW computing and DL
+// loader wavefronts, K a whole number of 8-step stages (checked by the launcher).
+template <typename T, int AR, int BC>
+__global__ __launch_bounds__((SkinnyTile<T, AR, BC>::DTHREADS)) void skinny_deep_kernel(BmmArgs args) {
+  using S = SkinnyTile<T, AR, BC>;
+  static_assert(S::DEEP && AR <= 32, "loader-split blocks of 32 rows");
+  __shared__ __attribute__((aligned(16))) char smem[S::DLDS_BYTES];
+  const uint32_t t = (uint32_t)xcd_slot(blockIdx.x, gridDim.x);
+  if (t >= (uint32_t)args.total) return;
+  const TileOrigin o = tile_origin(args, t, 32, BC);
+  const T* A = reinterpret_cast<const T*>(args.A) + o.b1 * args.sA1 + o.b2 * args.sA2 + o.m0 * args.lda;
+  const T* B = reinterpret_cast<const T*>(args.B) + o.b1 * args.sB1 +
+               (o.b2 / (uint32_t)args.gB) * args.sB2 + o.n0 * args.ldb;
+  const int64_t rows64 = o.m_end - o.m0, cols64 = args.N - o.n0;
+  const int rows = rows64 < 32 ? (int)rows64 : 32;
+  const int cols = cols64 < BC ? (int)cols64 : BC;
+  const typename S::Acc acc = S::run_deep(smem, A, args.lda, rows, B, args.ldb, cols, args.K / S::BK);
+  skinny_store<S, T>(args, o, rows, cols, acc);
 }
 
 template <typename T, int BM, int BN, int SB, bool BKM>
@@ -418,8 +445,15 @@ static int launch_skinny_block(const BmmArgs& a0, hipStream_t stream) {
   // a whole number of workgroups per XCD, so that xcd_slot keeps neighbouring blocks (which
   // share A rows and B columns) on one XCD; the extra workgroups exit at once
   const int64_t grid = (a.total + 7) & ~int64_t(7);
-  hipLaunchKernelGGL((skinny_kernel<T, AR, BC>), dim3((unsigned)grid),
-                     dim3(SkinnyTile<T, AR, BC>::THREADS), 0, stream, a);
+  using S = SkinnyTile<T, AR, BC>;
+  if constexpr (S::DEEP) {
+    const int64_t kt = a.K / S::BK;
+    if (kt % S::UD == 0) {
+      hipLaunchKernelGGL((skinny_deep_kernel<T, AR, BC>), dim3((unsigned)grid), dim3(S::DTHREADS), 0, stream, a);
+      return check_launch("skinny_deep_kernel");
+    }
+  }
+  hipLaunchKernelGGL((skinny_kernel<T, AR, BC>), dim3((unsigned)grid), dim3(S::THREADS), 0, stream, a);
   return check_launch("skinny_kernel");
 }
 

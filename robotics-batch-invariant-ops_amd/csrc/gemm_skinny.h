@@ -349,6 +349,138 @@ struct SkinnyTile {
     wait_loads<0>();
     return acc;
   }
+
+  // ---- Loader-split schedule with fragments read three pairs ahead ----
+  // For blocks whose computing wavefronts each hold one 16 x 16 accumulator (16-bit types, at
+  // most 16 rows and 16 columns per wavefront) the time of run() is the computing wavefronts'
+  // chain: every pair of K steps waited for the LDS reads issued during the pair before it.
+  // A global->LDS load in flight makes the compiler wait for every outstanding LDS read
+  // (lgkmcnt(0)) before a fragment is used, so reads issued further ahead would be waited for
+  // just as early.  Here DL loader wavefronts (after the CW computing ones) issue every load,
+  // and the computing wavefronts, with no such load on their path, read the fragments of pair
+  // p + 3 while pair p runs (four register sets) and the compiler waits for each set alone.
+  // Stages hold UD = 8 K steps in a ring of DSTAGES = 4 slots; barrier t (t = 1 .. NS-1),
+  // which the computing wavefronts reach at pair 1 of stage t-1, publishes stage t and refills
+  // the slot of stage t-2, whose fragments are all in registers by then, so it needs no LDS
+  // wait.  The MFMAs run in run()'s order (K step pairs in order, quads in order), so the bits
+  // are those of every other entry.  Measured on MI355X (bf16, one row, launches back to back,
+  // weights in the last-level cache): N = 8192, K = 2048 (8 x 32 blocks) 5.57 -> 4.61 us;
+  // N = 2048, K = 8192 (8 x 8 blocks) 8.09 -> 5.98 us (four loader wavefronts: 4.77 / 6.00 us).
+  // Blocks whose 8-step stages leave room for only three slots (16 x 32, 32 x 16: one stage in
+  // flight) measured slower (M = 16, N = 8192, K = 2048 6.2 -> 7.1 us; M = 64, N = 2048,
+  // K = 8192 11.5 -> 16.1 us) and keep run(), as does K that is not a whole number of stages.
+  static constexpr int DL = 8;                     // loader wavefronts
+  static constexpr int DTHREADS = 64 * (CW + DL);
+  static constexpr int UD = 8;                     // K steps per stage
+  static constexpr int PPS = UD / 2;               // K step pairs per stage
+  static constexpr int DSETS = 4;                  // fragment sets (pairs) in registers
+  static constexpr int DA = DSETS - 1;             // read-ahead, in pairs
+  static constexpr int DSTAGE_BYTES = UD * LDS_KSTEP;
+  static constexpr int DSTAGES = 4;
+  static constexpr int DLDS_BYTES = DSTAGES * DSTAGE_BYTES;
+  static constexpr int DLOADS = UD * IPK / DL;     // loads per loader wavefront per stage
+  static constexpr bool DEEP = sizeof(T) == 2 && Math::COUNT == 2 && DLDS_BYTES <= 160 * 1024;
+  static_assert(!DEEP || (PPS == DSETS && UD * IPK % DL == 0 && (DSTAGES - 1) * DLOADS < 64 &&
+                          DTHREADS <= 1024), "deep schedule");
+
+  __device__ static __forceinline__ void barrier_only() {
+    asm volatile("" ::: "memory");  // compiler fence
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  __device__ static __forceinline__ void read_pair(const char* p, Frags2& g) {
+    load_frags(p, g.s[0]);
+    load_frags(p + LDS_KSTEP, g.s[1]);
+  }
+  // Pair f with the reads of the pair at `next` into g (g was last read by the previous pair's
+  // MFMAs).  The reads are unconditional, so that the compiler's count of outstanding reads is
+  // the same on every path; past the last stage they read ring bytes that nothing uses.
+  __device__ static __forceinline__ void deep_pair(Acc& acc, const Frags2& f, const char* next, Frags2& g) {
+    Math::one(acc, f.s[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_pair(next, g);
+    __builtin_amdgcn_sched_barrier(0);
+    Math::one(acc, f.s[0], 1);
+    mfma(acc, f.s[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // The block of run() on DTHREADS threads, KT a positive multiple of UD.  Returns the
+  // accumulator of computing wavefront w < CW (loader wavefronts return zeros).
+  __device__ static __forceinline__ Acc run_deep(char* smem, const T* A, int64_t lda, int rows,
+                                                 const T* B, int64_t ldb, int cols, int64_t KT) {
+    Acc acc;
+    Math::zero(acc);
+    if constexpr (DEEP) {
+      const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+      const int64_t NS = KT / UD;
+      if (w >= CW) {
+        // Loader li issues instructions li + DL*i of a stage (K step u, part p: A rows 8p..8p+7
+        // or B columns, as in run()).
+        const int li = w - CW;
+        const int lane = threadIdx.x & 63;
+        const T* src[DLOADS];
+        int ku[DLOADS];
+        int dst[DLOADS];
+#pragma unroll
+        for (int i = 0; i < DLOADS; ++i) {
+          const int ins = li + DL * i;
+          const int u = ins / IPK, p = ins % IPK;
+          const bool is_a = p < AR / 8;
+          const int part = is_a ? p : p - AR / 8;
+          const int r = 8 * part + (lane >> 3);
+          const int c = (lane & 7) ^ ((r >> 1) & 7);
+          src[i] = is_a ? A + (int64_t)(r < rows ? r : rows - 1) * lda + c * VEC
+                        : B + (int64_t)(r < cols ? r : cols - 1) * ldb + c * VEC;
+          ku[i] = u;
+          dst[i] = u * LDS_KSTEP + (is_a ? 0 : LDS_A) + part * 64 * 16;
+        }
+        auto issue = [&](int64_t stage) {  // stage < NS
+          char* buf = smem + (int)(stage % DSTAGES) * DSTAGE_BYTES;
+#pragma unroll
+          for (int i = 0; i < DLOADS; ++i)
+            __builtin_amdgcn_global_load_lds((global_cvoid_t*)(src[i] + (stage * UD + ku[i]) * BK),
+                                             (lds_void_t*)(buf + dst[i]), 16, 0, 0);
+        };
+#pragma unroll
+        for (int s = 0; s < DSTAGES - 1; ++s)
+          if (s < NS) issue(s);
+        if (NS >= DSTAGES - 1)
+          wait_loads<(DSTAGES - 2) * DLOADS>();  // stage 0 landed
+        else
+          wait_loads<0>();
+        barrier_only();  // publishes stage 0
+        for (int64_t t = 1; t < NS; ++t) {
+          // issued so far: stages 0 .. min(t + DSTAGES - 3, NS - 1)
+          if (t + DSTAGES - 3 < NS)
+            wait_loads<(DSTAGES - 3) * DLOADS>();  // stage t landed
+          else
+            wait_loads<0>();
+          barrier_only();
+          if (t + DSTAGES - 2 < NS) issue(t + DSTAGES - 2);  // into the slot of stage t-2
+        }
+        wait_loads<0>();
+        return acc;
+      }
+      barrier_only();  // stage 0 published
+      Frags2 F[DSETS];
+#pragma unroll
+      for (int i = 0; i < DA; ++i) read_pair(smem + 2 * i * LDS_KSTEP, F[i]);
+      for (int64_t s = 0; s < NS; ++s) {
+        const char* cur = smem + (int)(s % DSTAGES) * DSTAGE_BYTES;
+        const char* nxt = smem + (int)((s + 1) % DSTAGES) * DSTAGE_BYTES;
+#pragma unroll
+        for (int d = 0; d < PPS; ++d) {
+          // the reads of this pair reach stage s+1 from pair PPS - DA on
+          if (d == PPS - DA && s + 1 < NS) barrier_only();
+          const int rp = d + DA;
+          const char* next = rp < PPS ? cur + rp * 2 * LDS_KSTEP : nxt + (rp - PPS) * 2 * LDS_KSTEP;
+          deep_pair(acc, F[d], next, F[(d + DA) % DSETS]);
+        }
+      }
+    }
+    return acc;
+  }
 };
 
 }  // namespace biops

@@ -335,6 +335,57 @@ def test_skinny_block_widths_give_identical_bits(tile_menu, dtype, m, n):
     assert_bitwise(matmul_persistent(x, w.t()), ref_plain, "skinny entry, no bias")
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize(("m", "n", "k"), (
+    (1, 2048, 8192),     # 8 x 8 blocks, 16 stages of 8 K steps, one loader-split block per unit
+    (5, 8192, 2048),     # 8 x 32 blocks (four stages: the whole ring)
+    (8, 4090, 1024),     # 8 x 16 blocks, 10-column last block, two stages
+    (16, 2048, 4096),    # 16 x 8 blocks
+    (13, 2048, 512),     # 16 x 8 blocks, one stage (K = 512)
+    (16, 4000, 1536),    # 16 x 16 blocks, three stages
+    (32, 2048, 8192),    # 32 x 8 blocks, two computing wavefronts of 16 rows
+    (20, 1003, 1536),    # 32 x 8 blocks, 3-column last block, three stages
+    (16, 8192, 2048),    # 16 x 32 blocks: three-slot rings keep the one-pass kernel
+    (64, 2048, 2048),    # 32 x 16 blocks, two row blocks: likewise
+    (3, 2048, 8320),     # K not a whole number of 8-step stages: the one-pass kernel
+))
+def test_skinny_loader_split_gives_identical_bits(tile_menu, dtype, m, n, k):
+    """Blocks of up to 16 rows and 16 columns per computing wavefront run on loader wavefronts
+    with fragments read three K-step pairs ahead when K is a whole number of 8-step stages; the
+    stored rows keep the bits of entry 2, with and without a bias, of a call on the last row
+    alone and of the automatic choice."""
+    xc = randn(m, k, seed=5600 + m, dtype=dtype)
+    wc = randn(n, k, seed=5601 + n, dtype=dtype, scale=0.05)
+    bc = randn(n, seed=5602, dtype=dtype)
+    x, w, bias = gpu(xc, wc, bc)
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = matmul_persistent(x, w.t(), bias)
+    ref_plain = matmul_persistent(x, w.t())
+    assert tile_menu.biops_set_gemm_tile(SKINNY_ENTRY) == 0
+    assert_bitwise(matmul_persistent(x, w.t(), bias), ref, "skinny entry")
+    assert_bitwise(matmul_persistent(x, w.t()), ref_plain, "skinny entry, no bias")
+    assert_bitwise(matmul_persistent(x[m - 1:], w.t(), bias), ref[m - 1:], "skinny entry, last row")
+    assert tile_menu.biops_set_gemm_tile(-1) == 0
+    assert_bitwise(matmul_persistent(x, w.t(), bias), ref, "automatic choice")
+    absprod = oracle.gemm_abs(xc, wc.t()) + bc.double().abs()
+    assert_gemm_close(ref, oracle.linear(xc, wc, bc), absprod, k)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_skinny_loader_split_batched(tile_menu, dtype):
+    """Batched skinny blocks (three products of 4 x 2048 x 2048, and a shared weight matrix)
+    on the loader-split schedule keep the bits of entry 2."""
+    a = gpu(randn(3, 4, 2048, seed=5610, dtype=dtype))
+    b = gpu(randn(3, 2048, 2048, seed=5611, dtype=dtype) * 0.05)
+    assert tile_menu.biops_set_gemm_tile(2) == 0
+    ref = bmm_persistent(a, b)
+    ref_shared = bmm_persistent(a, b[:1].expand(3, -1, -1))
+    assert tile_menu.biops_set_gemm_tile(SKINNY_ENTRY) == 0
+    assert_bitwise(bmm_persistent(a, b), ref, "skinny entry, batched")
+    assert_bitwise(bmm_persistent(a, b[:1].expand(3, -1, -1)), ref_shared, "skinny entry, shared B")
+    assert tile_menu.biops_set_gemm_tile(-1) == 0
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 @pytest.mark.parametrize(("m", "n", "k"), (
     (256, 2048, 2048),   # 8 row blocks x 32 blocks of 64 columns: one round
