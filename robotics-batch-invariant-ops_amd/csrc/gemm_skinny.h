@@ -462,10 +462,22 @@ struct SkinnyTile {
         wait_loads<0>();
         return acc;
       }
+      // Nothing of this wavefront is outstanding, but the compiler may join this path with the
+      // loaders' (their loads still counted as pending), which would make it wait for every LDS
+      // read at the loop head; the explicit wait gives the loop a clean count.  (With the one
+      // drain per stage that this and the read order below remove, the shapes above measured
+      // the same: their time is the chain of dependent MFMAs, about 30 cycles a link.)
+      __builtin_amdgcn_s_waitcnt(0);
       barrier_only();  // stage 0 published
+      // Pairs 0 .. DA-1 read in order (the scheduling barriers keep the compiler from reversing
+      // them), so that on entry, as on every later pass, the set of the loop's first pair is
+      // the oldest of the outstanding reads and its wait leaves the younger ones in flight.
       Frags2 F[DSETS];
 #pragma unroll
-      for (int i = 0; i < DA; ++i) read_pair(smem + 2 * i * LDS_KSTEP, F[i]);
+      for (int i = 0; i < DA; ++i) {
+        read_pair(smem + 2 * i * LDS_KSTEP, F[i]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       for (int64_t s = 0; s < NS; ++s) {
         const char* cur = smem + (int)(s % DSTAGES) * DSTAGE_BYTES;
         const char* nxt = smem + (int)((s + 1) % DSTAGES) * DSTAGE_BYTES;
