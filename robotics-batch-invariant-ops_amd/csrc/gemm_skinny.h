@@ -363,12 +363,15 @@ struct SkinnyTile {
   // which the computing wavefronts reach at pair 1 of stage t-1, publishes stage t and refills
   // the slot of stage t-2, whose fragments are all in registers by then, so it needs no LDS
   // wait.  The MFMAs run in run()'s order (K step pairs in order, quads in order), so the bits
-  // are those of every other entry.  Measured on MI355X (bf16, one row, launches back to back,
-  // weights in the last-level cache): N = 8192, K = 2048 (8 x 32 blocks) 5.57 -> 4.61 us;
-  // N = 2048, K = 8192 (8 x 8 blocks) 8.09 -> 5.98 us (four loader wavefronts: 4.77 / 6.00 us).
-  // Blocks whose 8-step stages leave room for only three slots (16 x 32, 32 x 16: one stage in
-  // flight) measured slower (M = 16, N = 8192, K = 2048 6.2 -> 7.1 us; M = 64, N = 2048,
-  // K = 8192 11.5 -> 16.1 us) and keep run(), as does K that is not a whole number of stages.
+  // are those of every other entry.  Measured on MI355X (bf16, same-box A/B against run(),
+  // launches back to back, weights in the last-level cache): one row, N = 8192, K = 2048 (8 x 32
+  // blocks) 6.3 -> 5.7 us; N = 2048, K = 8192 (8 x 8 blocks) 7.8 -> 6.6 us, M = 32 (32 x 8)
+  // 11.6 -> 10.4 us.  Blocks whose 8-step stages leave room for only three slots (16 x 32,
+  // 32 x 16, 32 x 32) keep run(): with three slots (one stage in flight) M = 16, N = 8192,
+  // K = 2048 took 6.2 -> 7.1 us and M = 64, N = 2048, K = 8192 11.5 -> 16.1 us, and with 4-step
+  // stages in rings of five or six slots 6.3 -> 6.8, 11.7 -> 12.6 and, for 32 x 32 blocks,
+  // M = 32, N = 8192 6.9 -> 7.8 us and M = 128, N = 2048, K = 8192 14.1 -> 16.5 us.  K that is
+  // not a whole number of stages keeps run() as well.
   static constexpr int DL = 8;                     // loader wavefronts
   static constexpr int DTHREADS = 64 * (CW + DL);
   static constexpr int UD = 8;                     // K steps per stage
