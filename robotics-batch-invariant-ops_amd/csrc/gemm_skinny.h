@@ -371,7 +371,9 @@ struct SkinnyTile {
   // K = 2048 took 6.2 -> 7.1 us and M = 64, N = 2048, K = 8192 11.5 -> 16.1 us, and with 4-step
   // stages in rings of five or six slots 6.3 -> 6.8, 11.7 -> 12.6 and, for 32 x 32 blocks,
   // M = 32, N = 8192 6.9 -> 7.8 us and M = 128, N = 2048, K = 8192 14.1 -> 16.5 us.  K that is
-  // not a whole number of stages keeps run() as well.
+  // not a whole number of stages keeps run() as well.  Filling all four slots up front (the
+  // last stage of a K = 2048 block then issued with the others) measured slower: one row,
+  // N = 8192, K = 2048 5.6 -> 5.7 us, M = 8, N = 4096, K = 1024 4.2 -> 4.5 us.
   static constexpr int DL = 8;                     // loader wavefronts
   static constexpr int DTHREADS = 64 * (CW + DL);
   static constexpr int UD = 8;                     // K steps per stage
