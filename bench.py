@@ -115,6 +115,18 @@ def profile_kernel(which, iters):
         x = torch.randn(1024, k, generator=g).to(torch.bfloat16).cuda()
         for _ in range(iters):
             linear_batch_invariant(x, w)
+    elif which in ("gemm_m1", "gemm_m1_long"):
+        # one row through the configs[1] linears: gemm_m1 the 2048->8192 one (+bias),
+        # gemm_m1_long the 8192->2048 one (the skinny entry's loader-split schedule)
+        from batch_invariant_ops import linear_batch_invariant
+
+        g = torch.Generator().manual_seed(20)
+        n, k, has_bias = SHAPES[0] if which == "gemm_m1" else SHAPES[1]
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).cuda() if has_bias else None
+        x = torch.randn(1, k, generator=g).to(torch.bfloat16).cuda()
+        for _ in range(iters):
+            linear_batch_invariant(x, w, b)
     elif which == "c1":
         # the README's fp32 mm, 2048x4096 . 4096x4096 (linspace operands, B row-major)
         a = torch.linspace(-100, 100, 2048 * 4096, device="cuda").reshape(2048, 4096)
@@ -161,7 +173,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument(
         "--profile-kernel",
-        choices=("gemm", "gemm_mid", "copy", "c1", "sdpa", "varlen", "moe", "moe_t1", "moe_t256", "softmax", "norm",
+        choices=("gemm", "gemm_mid", "gemm_m1", "gemm_m1_long", "copy", "c1", "sdpa", "varlen", "moe", "moe_t1", "moe_t256", "softmax", "norm",
                  "mean_c2", "norm_c2"),
         default=None,
         help="only launch the roofline kernel (gemm), the M=1024 8192->2048 linear (gemm_mid), a "
